@@ -1,0 +1,269 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X kernel surface at BASELINE.json's configurations.
+
+The headline line measures configs[1] (the GPT-2-small memory-bound set), which fits one GPU:
+one "step" is one pass of GELU fwd (bf16 [8,1024,3072]), sparse cross-entropy fwd and bwd
+(fp32 [8192, 50257]), GELU bwd and one multi-tensor AdamW step over the 148 GPT-2-small
+tensors (124,439,808 fp32 parameters), in that order so that no kernel finds its inputs in the
+256 MB last-level cache from the previous one. `value` = algorithmic bytes of the step / step
+time (GB/s, the reference's byte conventions, README.md:186-199).
+
+`roofline` is for the step's dominant kernel (longest average duration), timed live with HIP
+events on the launch stream. `cpu_baseline` is the repository's CPU oracle (a restatement of
+the reference harnesses' CPU references) timed on this host on a bounded sample of the same
+step. `per_kernel` lists each kernel of the surface at its BASELINE config, timed alone
+(cache flushed between repetitions).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--suite headline|all]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+
+def _args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--suite", choices=["headline", "all"], default="all")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--reps", type=int, default=20, help="repetitions per per-kernel timing")
+    return ap.parse_args()
+
+
+ARGS = _args()
+if ARGS.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+    print("bench.py: this build measures one GPU only (every kernel runs on one MI355X; "
+          "see DESIGN.md for how the surface would shard). Run with --gpus 1.", file=sys.stderr)
+    sys.exit(2)
+
+import torch  # noqa: E402
+
+from hyperkernels_amd import kernels as hk  # noqa: E402
+from hyperkernels_amd import workloads as W  # noqa: E402
+
+DEV = torch.device("cuda", 0)
+torch.cuda.set_device(DEV)
+hk.lib()  # fail loudly if the HIP library is missing
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+class Flusher:
+    """Writes 512 MiB between repetitions so a timed kernel starts with a cold L2 and MALL."""
+
+    def __init__(self):
+        self.buf = torch.empty(512 << 20, dtype=torch.uint8, device=DEV)
+
+    def __call__(self):
+        self.buf.fill_(1)
+
+
+def time_kernel(fn, reps, flush=None):
+    """Average duration (ms) of fn's launches, each bracketed by events on the current stream."""
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    fn()
+    torch.cuda.synchronize()
+    for i in range(reps):
+        if flush:
+            flush()
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    ts = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    return {"avg_ms": sum(ts) / len(ts), "median_ms": ts[len(ts) // 2], "min_ms": ts[0]}
+
+
+# ------------------------------------------------------------------------------------------------
+# headline step: configs[1]
+# ------------------------------------------------------------------------------------------------
+def make_step():
+    g = torch.Generator(device=DEV)
+    g.manual_seed(1234)
+    n = 8 * 1024 * 3072
+    gx = torch.randn(n, generator=g, device=DEV).to(torch.bfloat16)
+    gdy = torch.randn(n, generator=g, device=DEV).to(torch.bfloat16)
+    gy = torch.empty_like(gx)
+    gdx = torch.empty_like(gx)
+    R, V = W.CE["rows"], W.CE["vocab"]
+    logits = torch.randn(R, V, generator=g, device=DEV) * 2.0
+    targets = torch.randint(0, V, (R,), generator=g, device=DEV, dtype=torch.int32)
+    loss = torch.empty(R, device=DEV)
+    mx = torch.empty(R, device=DEV)
+    sm = torch.empty(R, device=DEV)
+    grad = torch.empty_like(logits)
+    gout = torch.ones(1, device=DEV)
+    shapes = W.gpt2_param_shapes()
+    P = [torch.randn(W.numel(s), generator=g, device=DEV) * 0.02 for s in shapes]
+    G = [torch.randn(W.numel(s), generator=g, device=DEV) * 1e-2 for s in shapes]
+    M = [torch.rand(W.numel(s), generator=g, device=DEV) * 0.1 for s in shapes]
+    Vv = [torch.rand(W.numel(s), generator=g, device=DEV) * 0.1 for s in shapes]
+    plan = hk.AdamPlan(P, G, M, Vv)
+    c = W.ADAMW
+    hyper = (c["lr"], c["beta1"], c["beta2"], c["eps"], c["weight_decay"], 1 - c["beta1"],
+             1 - c["beta2"])
+    ks = [
+        ("gelu_fwd_bf16", lambda: hk.gelu_forward(gx, gy), W.gelu_fwd_bytes(n, 2)),
+        ("ce_fwd", lambda: hk.sparse_ce_forward(logits, targets, loss, mx, sm), W.ce_fwd_bytes(R, V)),
+        ("ce_bwd", lambda: hk.sparse_ce_backward(logits, targets, mx, sm, gout, 1.0, grad),
+         W.ce_bwd_bytes(R, V)),
+        ("gelu_bwd_bf16", lambda: hk.gelu_backward(gdy, gx, gdx), W.gelu_bwd_bytes(n, 2)),
+        ("adamw_148", lambda: plan.step(*hyper), W.adamw_bytes(W.GPT2_NUM_PARAMS)),
+    ]
+    return ks, (plan, P, G, M, Vv)
+
+
+def run_headline():
+    ks, keep = make_step()
+    step_bytes = sum(b for _, _, b in ks)
+    names = [k for k, _, _ in ks]
+    for _ in range(ARGS.warmup):
+        for _, f, _ in ks:
+            f()
+    torch.cuda.synchronize()
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in ks] for _ in range(ARGS.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(ARGS.steps):
+        for (a, b), (_, f, _) in zip(ev[s], ks):
+            a.record()
+            f()
+            b.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = {n: sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(ARGS.steps)) / ARGS.steps
+           for i, n in enumerate(names)}
+    del keep
+    return ks, step_bytes, wall / ARGS.steps * 1e3, per
+
+
+# ------------------------------------------------------------------------------------------------
+# CPU baseline: the oracle on a bounded sample of the step
+# ------------------------------------------------------------------------------------------------
+def run_cpu_baseline():
+    import oracle
+
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = max(1, min(cores, 16))
+    oracle.set_threads(cores)
+    n = 8 * 1024 * 3072 // 4
+    x = oracle.f32_to_bf16(oracle.normal(n, 1))
+    dy = oracle.f32_to_bf16(oracle.normal(n, 2))
+    rows, V = 512, W.CE["vocab"]
+    logits = oracle.normal(rows * V, 3, 0.0, 2.0).reshape(rows, V)
+    targets = (np.arange(rows) * 7919 % V).astype(np.int32)
+    P = W.GPT2_NUM_PARAMS // 8
+    p, g = oracle.normal(P, 4, 0, 0.02), oracle.normal(P, 5, 0, 1e-2)
+    m, v = oracle.splitmix_uniform(P, 6, 0, 0.1), oracle.splitmix_uniform(P, 7, 0, 0.1)
+    c = W.ADAMW
+    t0 = time.perf_counter()
+    y = oracle.gelu_forward(x)
+    loss, mx, sm = oracle.sparse_ce_forward(logits, targets)
+    gr = oracle.sparse_ce_backward(logits, targets, mx, sm, 1.0)
+    gi = oracle.gelu_backward(dy, x)
+    oracle.adamw(p, g, m, v, c["lr"], c["beta1"], c["beta2"], c["eps"], c["weight_decay"],
+                 1 - c["beta1"], 1 - c["beta2"])
+    dt = time.perf_counter() - t0
+    del y, gr, gi
+    nbytes = (W.gelu_fwd_bytes(n, 2) + W.gelu_bwd_bytes(n, 2) + W.ce_fwd_bytes(rows, V)
+              + W.ce_bwd_bytes(rows, V) + W.adamw_bytes(P))
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": (f"oracle (C++ restatement of the reference CPU references) on 1/4 of the GELU "
+                       f"elements, {rows} of 8192 CE rows, 1/8 of the AdamW params; "
+                       f"{dt:.2f} s on {cores} threads")}
+
+
+# ------------------------------------------------------------------------------------------------
+# per-kernel suite
+# ------------------------------------------------------------------------------------------------
+def per_kernel_suite(flush):
+    out = {}
+    g = torch.Generator(device=DEV)
+    g.manual_seed(99)
+    # LayerNorm configs[0]
+    R, C = W.LN["rows"], W.LN["cols"]
+    x = torch.randn(R, C, generator=g, device=DEV)
+    gamma = torch.rand(C, generator=g, device=DEV) + 0.5
+    beta = torch.randn(C, generator=g, device=DEV) * 0.1
+    dy = torch.randn(R, C, generator=g, device=DEV)
+    y, mean, rstd = hk.layer_norm_forward(x, gamma, beta, W.LN["eps"])
+    dx = torch.empty_like(x)
+    dgam = torch.zeros(C, device=DEV)
+    dbet = torch.zeros(C, device=DEV)
+    cases = [
+        ("ln_fwd", lambda: hk.layer_norm_forward(x, gamma, beta, W.LN["eps"], y, mean, rstd),
+         W.ln_fwd_bytes(R, C), "hbm"),
+        ("ln_bwd_fused", lambda: hk.layer_norm_backward(dy, x, mean, rstd, gamma, dgam, dbet, dx),
+         W.ln_bwd_bytes(R, C), "hbm"),
+    ]
+    # unified reduce at the README shape
+    rs = torch.randn(16384, 50304, generator=g, device=DEV)
+    lay = hk.ReductionLayout()
+    lay.path, lay.num_outputs, lay.reduced_count = hk.REDUCE_INNER, 16384, 50304
+    lay.input_outer_stride = 50304
+    rdst = torch.empty(16384, device=DEV)
+    cases.append(("reduce_inner_16384x50304", lambda: hk.unified_reduce_sum(rs, lay, rdst),
+                  16384 * 50304 * 4, "hbm"))
+    for name, fn, work, bound in cases:
+        t = time_kernel(fn, ARGS.reps, flush)
+        ach = work / (t["avg_ms"] * 1e-3) / 1e9
+        out[name] = {"avg_ms": round(t["avg_ms"], 5), "achieved": round(ach, 1), "unit": "GB/s",
+                     "frac": round(ach / W.PEAK_HBM_GBS, 4)}
+        log(name, out[name])
+    return out
+
+
+def main():
+    log(f"device: {torch.cuda.get_device_name(0)}")
+    ks, step_bytes, ms_step, per = run_headline()
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    byte_of = {n: b for n, _, b in ks}
+    dom = max(per, key=per.get)
+    ach = byte_of[dom] / (per[dom] * 1e-3) / 1e9
+    for n in per:
+        log(f"step kernel {n}: {per[n]:.4f} ms, {byte_of[n] / (per[n] * 1e-3) / 1e9:.1f} GB/s")
+    result = {
+        "metric": "TFLOP/s (attn, GEMM) & GB/s (LN/GELU/CE/Adam) vs MI355X roofline",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": ARGS.steps,
+        "warmup": ARGS.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "configs[1] GPT-2-small memory-bound set: GELU(tanh) fwd+bwd bf16 "
+                               "[8,1024,3072]; sparse CE fwd+bwd fp32 [8192,50257] int32 targets; "
+                               "multi-tensor AdamW 148 tensors / 124,439,808 fp32 params",
+                   "step_bytes": step_bytes},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1),
+                     "peak": W.PEAK_HBM_GBS, "unit": "GB/s", "frac": round(ach / W.PEAK_HBM_GBS, 4),
+                     "traffic": None},
+    }
+    if ARGS.suite == "all":
+        result["per_kernel"] = {n: {"avg_ms": round(per[n], 5),
+                                    "achieved": round(byte_of[n] / (per[n] * 1e-3) / 1e9, 1),
+                                    "unit": "GB/s"} for n in per}
+        result["per_kernel"].update(per_kernel_suite(Flusher()))
+    if not ARGS.no_cpu:
+        result["cpu_baseline"] = run_cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,232 @@
+// adamw.hip - multi-tensor Adam/AdamW step over fp32 parameters.
+//
+// Reference behaviour: kernels/optimizer/multi_tensor_adam_sm89_kernel.cu:23-113. Per element,
+// in this exact operation order (the order fixes the rounding, so results match the CPU
+// oracle bit for bit):
+//   m' = fmaf(b1, m, (1 - b1) * g)
+//   v' = fmaf(b2, v, ((1 - b2) * g) * g)
+//   p' = p - lr * ((m' / bc1) / (sqrtf(v' / bc2) + eps) + wd * p)
+// FMA contraction is disabled in the update so that only the two explicit fmaf calls fuse,
+// and division and square root are the correctly rounded IEEE operations.
+//
+// Two front ends share the update:
+//   - hk_multi_tensor_adam: the reference's by-value launch metadata (<= 48 tensors,
+//     <= 320 chunks of 32768 elements per launch).
+//   - the plan API: the tensor table and chunk table of any number of tensors live in device
+//     memory, built once, so a whole-model step (GPT-2 small: 148 tensors, 3,892 chunks) is a
+//     single launch with no host-to-device traffic.
+// Each workgroup streams one chunk: a scalar head up to the first 16-byte boundary, 16-byte
+// loads of p, g, m, v in the body (two iterations in flight per lane), and a scalar tail. A
+// tensor whose four arrays do not share the same 16-byte phase is processed scalar.
+#include <vector>
+
+#include "hk_device.h"
+#include "hk_host.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+struct AdamHyper {
+  float lr, beta1, beta2, eps, wd, bc1, bc2;
+};
+
+#pragma clang fp contract(off)
+__device__ __forceinline__ void adam_update(float& p, float g, float& m, float& v,
+                                            const AdamHyper& h) {
+  const float m_new = __builtin_fmaf(h.beta1, m, (1.0f - h.beta1) * g);
+  const float v_new = __builtin_fmaf(h.beta2, v, (1.0f - h.beta2) * g * g);
+  const float denom = __builtin_sqrtf(v_new / h.bc2) + h.eps;
+  p = p - h.lr * ((m_new / h.bc1) / denom + h.wd * p);
+  m = m_new;
+  v = v_new;
+}
+#pragma clang fp contract(on)
+
+__device__ __forceinline__ void adam_update4(float4& p, const float4& g, float4& m, float4& v,
+                                             const AdamHyper& h) {
+  adam_update(p.x, g.x, m.x, v.x, h);
+  adam_update(p.y, g.y, m.y, v.y, h);
+  adam_update(p.z, g.z, m.z, v.z, h);
+  adam_update(p.w, g.w, m.w, v.w, h);
+}
+
+__device__ __forceinline__ int phase16(const float* p) {
+  return static_cast<int>((reinterpret_cast<uintptr_t>(p) >> 2) & 3);
+}
+
+// Updates elements [start, end) of one tensor.
+__device__ __forceinline__ void adam_chunk(float* __restrict__ p, const float* __restrict__ g,
+                                           float* __restrict__ m, float* __restrict__ v,
+                                           int64_t start, int64_t end, const AdamHyper& h) {
+  const int ph = phase16(p);
+  const bool vec = ph == phase16(g) && ph == phase16(m) && ph == phase16(v);
+  int64_t vs = end, ve = end;
+  if (vec) {
+    vs = start + ((4 - ((ph + start) & 3)) & 3);
+    ve = end - ((ph + end) & 3);
+    if (vs > ve) vs = ve = end;
+  }
+  // scalar head [start, vs) and, when not vectorised, the whole range
+  const int64_t head_end = vec ? vs : end;
+  for (int64_t i = start + threadIdx.x; i < head_end; i += kThreads) {
+    float pi = p[i], mi = m[i], vi = v[i];
+    adam_update(pi, g[i], mi, vi, h);
+    p[i] = pi; m[i] = mi; v[i] = vi;
+  }
+  if (!vec) return;
+  float4* p4 = reinterpret_cast<float4*>(p + vs);
+  const float4* g4 = reinterpret_cast<const float4*>(g + vs);
+  float4* m4 = reinterpret_cast<float4*>(m + vs);
+  float4* v4 = reinterpret_cast<float4*>(v + vs);
+  const int64_t nv = (ve - vs) >> 2;
+  int64_t i = threadIdx.x;
+  for (; i + kThreads < nv; i += 2 * kThreads) {
+    float4 pa = p4[i], ga = hk::ld_nt(g4 + i), ma = m4[i], va = v4[i];
+    float4 pb = p4[i + kThreads], gb = hk::ld_nt(g4 + i + kThreads),
+           mb = m4[i + kThreads], vb = v4[i + kThreads];
+    adam_update4(pa, ga, ma, va, h);
+    adam_update4(pb, gb, mb, vb, h);
+    p4[i] = pa; m4[i] = ma; v4[i] = va;
+    p4[i + kThreads] = pb; m4[i + kThreads] = mb; v4[i + kThreads] = vb;
+  }
+  for (; i < nv; i += kThreads) {
+    float4 pa = p4[i], ga = g4[i], ma = m4[i], va = v4[i];
+    adam_update4(pa, ga, ma, va, h);
+    p4[i] = pa; m4[i] = ma; v4[i] = va;
+  }
+  for (int64_t j = ve + threadIdx.x; j < end; j += kThreads) {
+    float pj = p[j], mj = m[j], vj = v[j];
+    adam_update(pj, g[j], mj, vj, h);
+    p[j] = pj; m[j] = mj; v[j] = vj;
+  }
+}
+
+// ---- reference metadata front end -------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void adam_meta_kernel(hk_adam_launch_metadata meta,
+                                                             AdamHyper h) {
+  const int b = blockIdx.x;
+  if (b >= HK_ADAM_MAX_BLOCKS) return;
+  const int t = meta.block_to_tensor[b];
+  const int64_t numel = meta.sizes[t];
+  const int64_t start = static_cast<int64_t>(meta.block_to_chunk[b]) * HK_ADAM_CHUNK_SIZE;
+  int64_t end = start + HK_ADAM_CHUNK_SIZE;
+  if (end > numel) end = numel;
+  if (start >= end) return;
+  adam_chunk(meta.params[t], meta.grads[t], meta.ms[t], meta.vs[t], start, end, h);
+}
+
+// ---- plan front end ------------------------------------------------------------------------
+struct TensorEntry {
+  float* p;
+  float* g;
+  float* m;
+  float* v;
+  int64_t numel;
+};
+struct ChunkEntry {
+  int32_t tensor;
+  int32_t chunk;
+};
+
+__global__ __launch_bounds__(kThreads) void adam_plan_kernel(const TensorEntry* __restrict__ tensors,
+                                                             const ChunkEntry* __restrict__ chunks,
+                                                             AdamHyper h) {
+  const ChunkEntry c = chunks[blockIdx.x];
+  const TensorEntry t = tensors[c.tensor];
+  const int64_t start = static_cast<int64_t>(c.chunk) * HK_ADAM_CHUNK_SIZE;
+  int64_t end = start + HK_ADAM_CHUNK_SIZE;
+  if (end > t.numel) end = t.numel;
+  if (start >= end) return;
+  adam_chunk(t.p, t.g, t.m, t.v, start, end, h);
+}
+
+}  // namespace
+
+struct hk_adam_plan {
+  TensorEntry* d_tensors = nullptr;
+  ChunkEntry* d_chunks = nullptr;
+  int64_t num_chunks = 0;
+  int device = 0;
+};
+
+extern "C" hipError_t hk_multi_tensor_adam(const hk_adam_launch_metadata* meta, int num_blocks,
+                                           float lr, float beta1, float beta2, float eps,
+                                           float weight_decay, float bias_correction1,
+                                           float bias_correction2, hipStream_t stream) {
+  HK_CHECK_ARG(meta != nullptr);
+  HK_CHECK_ARG(num_blocks >= 0 && num_blocks <= HK_ADAM_MAX_BLOCKS);
+  if (num_blocks == 0) return hipSuccess;
+  for (int b = 0; b < num_blocks; ++b) HK_CHECK_ARG(meta->block_to_tensor[b] < HK_ADAM_MAX_TENSORS);
+  const AdamHyper h{lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2};
+  hipLaunchKernelGGL(adam_meta_kernel, dim3(num_blocks), dim3(kThreads), 0, stream, *meta, h);
+  return hk::launch_status();
+}
+
+extern "C" hipError_t hk_adam_plan_create(int num_tensors, float* const* params,
+                                          float* const* grads, float* const* ms,
+                                          float* const* vs, const int64_t* sizes,
+                                          hk_adam_plan** plan_out) {
+  HK_CHECK_ARG(plan_out != nullptr);
+  *plan_out = nullptr;
+  HK_CHECK_ARG(num_tensors >= 0);
+  HK_CHECK_ARG(num_tensors == 0 || (params && grads && ms && vs && sizes));
+  std::vector<TensorEntry> tensors(num_tensors);
+  std::vector<ChunkEntry> chunks;
+  for (int t = 0; t < num_tensors; ++t) {
+    HK_CHECK_ARG(sizes[t] >= 0);
+    HK_CHECK_ARG(sizes[t] == 0 || (params[t] && grads[t] && ms[t] && vs[t]));
+    const int64_t nch = hk::ceil_div(sizes[t], HK_ADAM_CHUNK_SIZE);
+    HK_CHECK_ARG(nch <= INT32_MAX);
+    tensors[t] = TensorEntry{params[t], grads[t], ms[t], vs[t], sizes[t]};
+    for (int64_t c = 0; c < nch; ++c) chunks.push_back(ChunkEntry{t, static_cast<int32_t>(c)});
+  }
+  HK_CHECK_ARG(chunks.size() <= static_cast<size_t>(INT32_MAX));
+  hk_adam_plan* plan = new hk_adam_plan();
+  plan->num_chunks = static_cast<int64_t>(chunks.size());
+  hipError_t e = hipGetDevice(&plan->device);
+  if (e == hipSuccess && !tensors.empty())
+    e = hipMalloc(&plan->d_tensors, tensors.size() * sizeof(TensorEntry));
+  if (e == hipSuccess && !tensors.empty())
+    e = hipMemcpy(plan->d_tensors, tensors.data(), tensors.size() * sizeof(TensorEntry),
+                  hipMemcpyHostToDevice);
+  if (e == hipSuccess && !chunks.empty())
+    e = hipMalloc(&plan->d_chunks, chunks.size() * sizeof(ChunkEntry));
+  if (e == hipSuccess && !chunks.empty())
+    e = hipMemcpy(plan->d_chunks, chunks.data(), chunks.size() * sizeof(ChunkEntry),
+                  hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hk_adam_plan_destroy(plan);
+    return e;
+  }
+  *plan_out = plan;
+  return hipSuccess;
+}
+
+extern "C" hipError_t hk_adam_plan_step(const hk_adam_plan* plan, float lr, float beta1,
+                                        float beta2, float eps, float weight_decay,
+                                        float bias_correction1, float bias_correction2,
+                                        hipStream_t stream) {
+  HK_CHECK_ARG(plan != nullptr);
+  if (plan->num_chunks == 0) return hipSuccess;
+  const AdamHyper h{lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2};
+  hipLaunchKernelGGL(adam_plan_kernel, dim3(static_cast<unsigned>(plan->num_chunks)),
+                     dim3(kThreads), 0, stream, plan->d_tensors, plan->d_chunks, h);
+  return hk::launch_status();
+}
+
+extern "C" hipError_t hk_adam_plan_destroy(hk_adam_plan* plan) {
+  if (!plan) return hipSuccess;
+  hipError_t e = hipSuccess;
+  if (plan->d_tensors) e = hipFree(plan->d_tensors);
+  if (plan->d_chunks) {
+    const hipError_t e2 = hipFree(plan->d_chunks);
+    if (e == hipSuccess) e = e2;
+  }
+  delete plan;
+  return e;
+}
+
+extern "C" int64_t hk_adam_plan_num_chunks(const hk_adam_plan* plan) {
+  return plan ? plan->num_chunks : 0;
+}

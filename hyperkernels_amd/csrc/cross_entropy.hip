@@ -1,0 +1,199 @@
+// cross_entropy.hip - sparse softmax cross-entropy over fp32 logits [rows, vocab].
+//
+// Reference behaviour:
+//   forward   kernels/loss/sparse_ce_forward_kernel_vec_save_stats.cu:14-106
+//             per row: max, sum = sum_j exp(x_j - max) (streaming online softmax),
+//             loss = log(sum) + max - x[target]; saves max and sum for the backward.
+//   backward  kernels/loss/sparseCENormalize_from_stats.cu:7-49
+//             grad_j = (exp(x_j - max) / sum - [j == target]) * (*grad_output * host_scale)
+//
+// Design (gfx950): one 256-lane workgroup streams one row. A row of fp32 logits starts at
+// row * vocab * 4 bytes, which is only 4-byte aligned when vocab is odd (the GPT-2 vocabulary
+// 50257 is), so each row is split into a scalar head up to the next 16-byte boundary, a body
+// of 16-byte loads (each lane keeps 4 of them in flight), and a scalar tail. This is what lets
+// any vocab size work; the reference assumes vocab % 4 == 0. Each lane keeps an online
+// (max, sum) state, updated once per 4 values; lanes merge with 64-wide butterflies and the
+// four waves merge through LDS.
+#include "hk_device.h"
+#include "hk_host.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / HK_WAVE;
+constexpr int kUnroll = 4;
+
+__device__ __forceinline__ void absorb1(float& m, float& s, float v) {
+  if (v > m) {
+    s = s * __expf(m - v) + 1.0f;
+    m = v;
+  } else {
+    s += __expf(v - m);
+  }
+}
+
+__device__ __forceinline__ void absorb4(float& m, float& s, float4 v) {
+  const float mx = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+  if (mx > m) {
+    s *= __expf(m - mx);
+    m = mx;
+  }
+  s += (__expf(v.x - m) + __expf(v.y - m)) + (__expf(v.z - m) + __expf(v.w - m));
+}
+
+// Splits [0, n) of a row that starts at p into head [0, h), body [h, h + 4 nb), tail.
+__device__ __forceinline__ void split_row(const void* p, int64_t n, int64_t& h, int64_t& nb) {
+  const int64_t mis = (reinterpret_cast<uintptr_t>(p) >> 2) & 3;
+  h = (4 - mis) & 3;
+  if (h > n) h = n;
+  nb = (n - h) >> 2;
+}
+
+__global__ __launch_bounds__(kThreads) void ce_forward(const float* __restrict__ logits,
+                                                       const int32_t* __restrict__ targets,
+                                                       float* __restrict__ losses,
+                                                       float* __restrict__ saved_max,
+                                                       float* __restrict__ saved_sum,
+                                                       int64_t vocab) {
+  __shared__ float red_m[kWaves], red_s[kWaves];
+  const int64_t row = blockIdx.x;
+  const float* x = logits + row * vocab;
+  const int tid = threadIdx.x;
+  float m = -INFINITY, s = 0.f;
+
+  int64_t h, nb;
+  split_row(x, vocab, h, nb);
+  if (tid < h) absorb1(m, s, x[tid]);
+  const float4* body = reinterpret_cast<const float4*>(x + h);
+  int64_t i = tid;
+  for (; i + (kUnroll - 1) * kThreads < nb; i += kUnroll * kThreads) {
+    float4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) v[u] = hk::ld_nt(body + i + u * kThreads);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) absorb4(m, s, v[u]);
+  }
+  for (; i < nb; i += kThreads) absorb4(m, s, hk::ld_nt(body + i));
+  for (int64_t j = h + 4 * nb + tid; j < vocab; j += kThreads) absorb1(m, s, x[j]);
+
+  hk::wave_softmax_merge(m, s);
+  const int wave = tid >> 6;
+  if ((tid & 63) == 0) {
+    red_m[wave] = m;
+    red_s[wave] = s;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float fm = red_m[0], fs = red_s[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) hk::softmax_merge(fm, fs, red_m[w], red_s[w]);
+    saved_max[row] = fm;
+    saved_sum[row] = fs;
+    const int64_t t = static_cast<int64_t>(targets[row]);
+    const float xt = (t >= 0 && t < vocab) ? x[t] : __builtin_nanf("");
+    losses[row] = logf(fs) + fm - xt;
+  }
+}
+
+__device__ __forceinline__ float ce_grad1(float v, float mx, float inv_sum, float scale,
+                                          bool hit) {
+  return (__expf(v - mx) * inv_sum - (hit ? 1.0f : 0.0f)) * scale;
+}
+
+// Vector path: logits and grad share the same 16-byte phase on every row.
+__global__ __launch_bounds__(kThreads) void ce_backward(
+    const float* __restrict__ logits, const int32_t* __restrict__ targets,
+    float* __restrict__ grad, const float* __restrict__ saved_max,
+    const float* __restrict__ saved_sum, int64_t vocab, const float* __restrict__ grad_output,
+    float host_scale) {
+  const int64_t row = blockIdx.x;
+  const float* x = logits + row * vocab;
+  float* g = grad + row * vocab;
+  const int tid = threadIdx.x;
+  const float mx = saved_max[row];
+  const float inv_sum = 1.0f / saved_sum[row];
+  const float scale = (grad_output ? grad_output[0] : 1.0f) * host_scale;
+  const int64_t t = static_cast<int64_t>(targets[row]);
+
+  int64_t h, nb;
+  split_row(x, vocab, h, nb);
+  if (tid < h) g[tid] = ce_grad1(x[tid], mx, inv_sum, scale, tid == t);
+  const float4* xb = reinterpret_cast<const float4*>(x + h);
+  float4* gb = reinterpret_cast<float4*>(g + h);
+  const int64_t tb = t - h;  // target position relative to the body start
+  int64_t i = tid;
+  for (; i + (kUnroll - 1) * kThreads < nb; i += kUnroll * kThreads) {
+    float4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) v[u] = hk::ld_nt(xb + i + u * kThreads);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = 4 * (i + u * kThreads);
+      float4 o;
+      o.x = ce_grad1(v[u].x, mx, inv_sum, scale, j + 0 == tb);
+      o.y = ce_grad1(v[u].y, mx, inv_sum, scale, j + 1 == tb);
+      o.z = ce_grad1(v[u].z, mx, inv_sum, scale, j + 2 == tb);
+      o.w = ce_grad1(v[u].w, mx, inv_sum, scale, j + 3 == tb);
+      hk::st_nt(gb + i + u * kThreads, o);
+    }
+  }
+  for (; i < nb; i += kThreads) {
+    const float4 v = hk::ld_nt(xb + i);
+    const int64_t j = 4 * i;
+    float4 o;
+    o.x = ce_grad1(v.x, mx, inv_sum, scale, j + 0 == tb);
+    o.y = ce_grad1(v.y, mx, inv_sum, scale, j + 1 == tb);
+    o.z = ce_grad1(v.z, mx, inv_sum, scale, j + 2 == tb);
+    o.w = ce_grad1(v.w, mx, inv_sum, scale, j + 3 == tb);
+    hk::st_nt(gb + i, o);
+  }
+  for (int64_t j = h + 4 * nb + tid; j < vocab; j += kThreads)
+    g[j] = ce_grad1(x[j], mx, inv_sum, scale, j == t);
+}
+
+// Scalar path for a grad buffer whose 16-byte phase differs from the logits buffer's.
+__global__ __launch_bounds__(kThreads) void ce_backward_scalar(
+    const float* __restrict__ logits, const int32_t* __restrict__ targets,
+    float* __restrict__ grad, const float* __restrict__ saved_max,
+    const float* __restrict__ saved_sum, int64_t vocab, const float* __restrict__ grad_output,
+    float host_scale) {
+  const int64_t row = blockIdx.x;
+  const float* x = logits + row * vocab;
+  float* g = grad + row * vocab;
+  const float mx = saved_max[row];
+  const float inv_sum = 1.0f / saved_sum[row];
+  const float scale = (grad_output ? grad_output[0] : 1.0f) * host_scale;
+  const int64_t t = static_cast<int64_t>(targets[row]);
+  for (int64_t j = threadIdx.x; j < vocab; j += kThreads)
+    g[j] = ce_grad1(x[j], mx, inv_sum, scale, j == t);
+}
+
+}  // namespace
+
+extern "C" hipError_t hk_sparse_ce_forward_f32_i32(const float* logits, const int32_t* targets,
+                                                   float* losses, float* saved_max,
+                                                   float* saved_sum, int64_t batch_size,
+                                                   int64_t vocab_size, hipStream_t stream) {
+  HK_CHECK_ARG(batch_size >= 0 && vocab_size >= 1 && batch_size <= INT32_MAX);
+  if (batch_size == 0) return hipSuccess;
+  HK_CHECK_ARG(logits && targets && losses && saved_max && saved_sum);
+  hipLaunchKernelGGL(ce_forward, dim3(static_cast<unsigned>(batch_size)), dim3(kThreads), 0,
+                     stream, logits, targets, losses, saved_max, saved_sum, vocab_size);
+  return hk::launch_status();
+}
+
+extern "C" hipError_t hk_sparse_ce_backward_f32_i32(const float* logits, const int32_t* targets,
+                                                    float* grad, const float* saved_max,
+                                                    const float* saved_sum, int64_t batch_size,
+                                                    int64_t vocab_size, const float* grad_output,
+                                                    float host_scale, hipStream_t stream) {
+  HK_CHECK_ARG(batch_size >= 0 && vocab_size >= 1 && batch_size <= INT32_MAX);
+  if (batch_size == 0) return hipSuccess;
+  HK_CHECK_ARG(logits && targets && grad && saved_max && saved_sum);
+  const bool same_phase = ((reinterpret_cast<uintptr_t>(logits) ^
+                            reinterpret_cast<uintptr_t>(grad)) & 15u) == 0;
+  hipLaunchKernelGGL(same_phase ? ce_backward : ce_backward_scalar,
+                     dim3(static_cast<unsigned>(batch_size)), dim3(kThreads), 0, stream, logits,
+                     targets, grad, saved_max, saved_sum, vocab_size, grad_output, host_scale);
+  return hk::launch_status();
+}

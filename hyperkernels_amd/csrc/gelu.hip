@@ -1,0 +1,230 @@
+// gelu.hip - tanh-approximation GELU forward/backward, fp32 math, fp32 or bf16 I/O.
+//
+// Reference behaviour: kernels/gelu/gelu_forward_sm89_kernel.cu:19-22 (forward formula) and
+// kernels/gelu/gelu_backward_sm89_kernel.cu:24-30 (analytic derivative). The reference uses the
+// PTX tanh.approx instruction; this file evaluates tanh from the exponential,
+// tanh(u) = 1 - 2 / (exp(2u) + 1), whose absolute error stays near 1e-7 over the whole range
+// (the formula only enters as 1 + tanh and 1 - tanh^2, so absolute error is what matters).
+//
+// HBM layout: flat contiguous tensors. Each lane moves 16 bytes per access (8 bf16 or
+// 4 fp32) and a workgroup of 256 lanes covers UNROLL consecutive 4 KiB spans, so every wave
+// issues fully coalesced 1 KiB transactions.
+#include "hk_device.h"
+#include "hk_host.h"
+
+namespace {
+
+constexpr float kSqrt2OverPi = 0.7978845608028654f;  // sqrt(2/pi)
+constexpr float kGeluCoef = 0.044715f;               // Hendrycks & Gimpel tanh fit
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+
+__device__ __forceinline__ float tanh_from_exp(float u) {
+  const float e = __expf(2.0f * u);
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+}
+
+__device__ __forceinline__ float gelu_fwd(float x) {
+  const float u = kSqrt2OverPi * (x + kGeluCoef * x * x * x);
+  return 0.5f * x * (1.0f + tanh_from_exp(u));
+}
+
+__device__ __forceinline__ float gelu_grad(float x) {
+  const float x2 = x * x;
+  const float u = kSqrt2OverPi * (x + kGeluCoef * x2 * x);
+  const float du = kSqrt2OverPi * (1.0f + 3.0f * kGeluCoef * x2);
+  const float th = tanh_from_exp(u);
+  return 0.5f * (1.0f + th) + 0.5f * x * (1.0f - th * th) * du;
+}
+
+// Element access for the two storage types.
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int kPerVec = 4;
+  __device__ static float load(const float* p, int64_t i) { return p[i]; }
+  __device__ static void store(float* p, int64_t i, float v) { p[i] = v; }
+  __device__ static void unpack(const uint4& r, float* f) {
+    f[0] = __uint_as_float(r.x); f[1] = __uint_as_float(r.y);
+    f[2] = __uint_as_float(r.z); f[3] = __uint_as_float(r.w);
+  }
+  __device__ static uint4 pack(const float* f) {
+    return make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
+                      __float_as_uint(f[3]));
+  }
+};
+template <> struct Elem<uint16_t> {
+  static constexpr int kPerVec = 8;
+  __device__ static float load(const uint16_t* p, int64_t i) { return hk::bf16_to_f32(p[i]); }
+  __device__ static void store(uint16_t* p, int64_t i, float v) { p[i] = hk::f32_to_bf16(v); }
+  __device__ static void unpack(const uint4& r, float* f) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      f[2 * k] = __uint_as_float(w[k] << 16);
+      f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+    }
+  }
+  __device__ static uint4 pack(const float* f) {
+    return make_uint4(hk::pack_bf16x2(f[0], f[1]), hk::pack_bf16x2(f[2], f[3]),
+                      hk::pack_bf16x2(f[4], f[5]), hk::pack_bf16x2(f[6], f[7]));
+  }
+};
+
+// Vector body: nvec 16-byte vectors, all pointers 16-byte aligned.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void gelu_fwd_vec(const uint4* __restrict__ in,
+                                                         uint4* __restrict__ out, int64_t nvec) {
+  constexpr int P = Elem<T>::kPerVec;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads * kUnroll + threadIdx.x;
+  uint4 r[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + u * kThreads;
+    if (i < nvec) r[u] = hk::ld_nt(in + i);
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + u * kThreads;
+    if (i < nvec) {
+      float f[P];
+      Elem<T>::unpack(r[u], f);
+#pragma unroll
+      for (int k = 0; k < P; ++k) f[k] = gelu_fwd(f[k]);
+      hk::st_nt(out + i, Elem<T>::pack(f));
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void gelu_bwd_vec(const uint4* __restrict__ grad,
+                                                         const uint4* __restrict__ in,
+                                                         uint4* __restrict__ grad_in,
+                                                         int64_t nvec) {
+  constexpr int P = Elem<T>::kPerVec;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads * kUnroll + threadIdx.x;
+  uint4 rg[kUnroll], rx[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + u * kThreads;
+    if (i < nvec) {
+      rg[u] = hk::ld_nt(grad + i);
+      rx[u] = hk::ld_nt(in + i);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + u * kThreads;
+    if (i < nvec) {
+      float g[P], x[P];
+      Elem<T>::unpack(rg[u], g);
+      Elem<T>::unpack(rx[u], x);
+#pragma unroll
+      for (int k = 0; k < P; ++k) g[k] = g[k] * gelu_grad(x[k]);
+      hk::st_nt(grad_in + i, Elem<T>::pack(g));
+    }
+  }
+}
+
+// Scalar path: tails and unaligned tensors.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void gelu_fwd_scalar(const T* __restrict__ in,
+                                                            T* __restrict__ out, int64_t begin,
+                                                            int64_t end) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t i = begin + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < end;
+       i += stride)
+    Elem<T>::store(out, i, gelu_fwd(Elem<T>::load(in, i)));
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void gelu_bwd_scalar(const T* __restrict__ grad,
+                                                            const T* __restrict__ in,
+                                                            T* __restrict__ grad_in,
+                                                            int64_t begin, int64_t end) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t i = begin + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < end;
+       i += stride)
+    Elem<T>::store(grad_in, i, Elem<T>::load(grad, i) * gelu_grad(Elem<T>::load(in, i)));
+}
+
+int scalar_grid(int64_t n) {
+  const int64_t blocks = hk::ceil_div(n, kThreads);
+  const int64_t cap = static_cast<int64_t>(hk::device_cu_count()) * 8;
+  return static_cast<int>(blocks < cap ? (blocks < 1 ? 1 : blocks) : cap);
+}
+
+template <typename T>
+hipError_t launch_fwd(const T* in, T* out, int64_t numel, hipStream_t stream) {
+  HK_CHECK_ARG(numel >= 0);
+  if (numel == 0) return hipSuccess;
+  HK_CHECK_ARG(in != nullptr && out != nullptr);
+  constexpr int P = Elem<T>::kPerVec;
+  int64_t done = 0;
+  if (hk::aligned16(in) && hk::aligned16(out)) {
+    const int64_t nvec = numel / P;
+    if (nvec > 0) {
+      const int64_t blocks = hk::ceil_div(nvec, int64_t(kThreads) * kUnroll);
+      HK_CHECK_ARG(blocks <= INT32_MAX);
+      hipLaunchKernelGGL(gelu_fwd_vec<T>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                         stream, reinterpret_cast<const uint4*>(in),
+                         reinterpret_cast<uint4*>(out), nvec);
+      HK_RETURN_IF_ERROR(hk::launch_status());
+    }
+    done = nvec * P;
+  }
+  if (done < numel) {
+    hipLaunchKernelGGL(gelu_fwd_scalar<T>, dim3(scalar_grid(numel - done)), dim3(kThreads), 0,
+                       stream, in, out, done, numel);
+    HK_RETURN_IF_ERROR(hk::launch_status());
+  }
+  return hipSuccess;
+}
+
+template <typename T>
+hipError_t launch_bwd(const T* grad, const T* in, T* grad_in, int64_t numel,
+                      hipStream_t stream) {
+  HK_CHECK_ARG(numel >= 0);
+  if (numel == 0) return hipSuccess;
+  HK_CHECK_ARG(grad != nullptr && in != nullptr && grad_in != nullptr);
+  constexpr int P = Elem<T>::kPerVec;
+  int64_t done = 0;
+  if (hk::aligned16(grad) && hk::aligned16(in) && hk::aligned16(grad_in)) {
+    const int64_t nvec = numel / P;
+    if (nvec > 0) {
+      const int64_t blocks = hk::ceil_div(nvec, int64_t(kThreads) * kUnroll);
+      HK_CHECK_ARG(blocks <= INT32_MAX);
+      hipLaunchKernelGGL(gelu_bwd_vec<T>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                         stream, reinterpret_cast<const uint4*>(grad),
+                         reinterpret_cast<const uint4*>(in), reinterpret_cast<uint4*>(grad_in),
+                         nvec);
+      HK_RETURN_IF_ERROR(hk::launch_status());
+    }
+    done = nvec * P;
+  }
+  if (done < numel) {
+    hipLaunchKernelGGL(gelu_bwd_scalar<T>, dim3(scalar_grid(numel - done)), dim3(kThreads), 0,
+                       stream, grad, in, grad_in, done, numel);
+    HK_RETURN_IF_ERROR(hk::launch_status());
+  }
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" hipError_t hk_gelu_forward_f32(const float* in, float* out, int64_t numel,
+                                          hipStream_t stream) {
+  return launch_fwd<float>(in, out, numel, stream);
+}
+extern "C" hipError_t hk_gelu_forward_bf16(const hk_bf16* in, hk_bf16* out, int64_t numel,
+                                           hipStream_t stream) {
+  return launch_fwd<uint16_t>(in, out, numel, stream);
+}
+extern "C" hipError_t hk_gelu_backward_f32(const float* grad, const float* in, float* grad_in,
+                                           int64_t numel, hipStream_t stream) {
+  return launch_bwd<float>(grad, in, grad_in, numel, stream);
+}
+extern "C" hipError_t hk_gelu_backward_bf16(const hk_bf16* grad, const hk_bf16* in,
+                                            hk_bf16* grad_in, int64_t numel,
+                                            hipStream_t stream) {
+  return launch_bwd<uint16_t>(grad, in, grad_in, numel, stream);
+}

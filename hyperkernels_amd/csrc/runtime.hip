@@ -1,0 +1,69 @@
+// runtime.hip - library-level state: ABI version, per-device facts and the device workspace.
+#include <mutex>
+#include <vector>
+
+#include "hk_host.h"
+
+extern "C" int hk_abi_version(void) { return HK_ABI_VERSION; }
+
+extern "C" const char* hk_error_string(hipError_t status) { return hipGetErrorString(status); }
+
+namespace hk {
+
+namespace {
+struct DeviceState {
+  int cu_count = 0;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+};
+std::mutex g_mu;
+std::vector<DeviceState> g_devices;
+
+DeviceState* state_for_current(hipError_t* err) {
+  int dev = 0;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  if (static_cast<int>(g_devices.size()) <= dev) g_devices.resize(dev + 1);
+  return &g_devices[dev];
+}
+}  // namespace
+
+int device_cu_count() {
+  std::lock_guard<std::mutex> lk(g_mu);
+  hipError_t e;
+  DeviceState* s = state_for_current(&e);
+  if (!s) return 256;
+  if (s->cu_count == 0) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        cus > 0)
+      s->cu_count = cus;
+    else
+      s->cu_count = 256;
+  }
+  return s->cu_count;
+}
+
+hipError_t device_workspace(size_t bytes, void** out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  hipError_t e;
+  DeviceState* s = state_for_current(&e);
+  if (!s) return e;
+  if (bytes > s->ws_bytes) {
+    if (s->ws) {
+      // Work already queued may still read the old buffer.
+      HK_RETURN_IF_ERROR(hipDeviceSynchronize());
+      HK_RETURN_IF_ERROR(hipFree(s->ws));
+      s->ws = nullptr;
+      s->ws_bytes = 0;
+    }
+    size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+    HK_RETURN_IF_ERROR(hipMalloc(&s->ws, want));
+    s->ws_bytes = want;
+  }
+  *out = s->ws;
+  return hipSuccess;
+}
+
+}  // namespace hk

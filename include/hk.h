@@ -1,0 +1,195 @@
+/*
+ * hk.h - C ABI of the MI355X (gfx950) transformer-training kernel surface.
+ *
+ * Every entry point replaces one kernel (or one family of template instantiations) of
+ * BlubridgeAI/HyperKernels. The reference kernels are templated `__global__` functions that
+ * the caller launches itself with `<<<grid, block, smem>>>`; here the library owns the launch
+ * geometry, so a caller passes only the problem arguments plus a stream. Template parameters
+ * (element type, layout, split-K, causal) become symbol suffixes or plain arguments.
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers (HBM) unless stated otherwise; the caller owns them.
+ *   - bf16 tensors and scalars are passed as raw bit patterns (`hk_bf16` = uint16_t).
+ *   - Matrices are row-major, as in the reference harnesses.
+ *   - The return value is the launch status. Nothing synchronises the stream.
+ *   - Preconditions that the kernels still need are validated and reported as
+ *     hipErrorInvalidValue; preconditions of the reference that this build lifts are listed
+ *     at each entry point.
+ */
+#ifndef HK_H_
+#define HK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Exported symbols of libhk_amd.so (the library is built with hidden default visibility). */
+#if defined(__GNUC__)
+#define HK_API __attribute__((visibility("default")))
+#else
+#define HK_API
+#endif
+
+typedef uint16_t hk_bf16;
+
+/* ------------------------------------------------------------------------------------------
+ * Library
+ * ---------------------------------------------------------------------------------------- */
+
+/* ABI version of this header; bumped on any incompatible change. */
+#define HK_ABI_VERSION 1
+HK_API int hk_abi_version(void);
+/* Text of a status returned by any entry point (hipGetErrorString of the library's runtime). */
+HK_API const char* hk_error_string(hipError_t status);
+
+/* ------------------------------------------------------------------------------------------
+ * GELU (tanh approximation), math in fp32, accurate tanh.
+ * Replaces gelu_forward_sm89_kernel<T>      (kernels/gelu/gelu_forward_sm89_kernel.cu:35-37)
+ *      and OwnTensor::cuda::gelu_backward_sm89_kernel<T>
+ *                                           (kernels/gelu/gelu_backward_sm89_kernel.cu:44-47).
+ * Any numel and any alignment (the reference needs float4 / bf16x2 alignment).
+ * ---------------------------------------------------------------------------------------- */
+HK_API hipError_t hk_gelu_forward_f32(const float* in, float* out, int64_t numel, hipStream_t stream);
+HK_API hipError_t hk_gelu_forward_bf16(const hk_bf16* in, hk_bf16* out, int64_t numel,
+                                hipStream_t stream);
+HK_API hipError_t hk_gelu_backward_f32(const float* grad, const float* in, float* grad_in,
+                                int64_t numel, hipStream_t stream);
+HK_API hipError_t hk_gelu_backward_bf16(const hk_bf16* grad, const hk_bf16* in, hk_bf16* grad_in,
+                                 int64_t numel, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * LayerNorm, fp32.
+ * Forward replaces layer_norm_forward_sm89_kernel<float,float>
+ *   (kernels/layernorm/layer_norm_forward_sm89_kernel.cu:27-32). The reference takes the row
+ *   count from gridDim.x; here it is the `rows` argument. gamma, beta, mean_out and rstd_out
+ *   may be NULL, as in the reference. Lifts the reference's blockDim == 512 requirement.
+ * Backward-input replaces OwnTensor::cuda::ln_backward_input_sm89_kernel<float>
+ *   (kernels/layernorm/ln_backward_input_sm89_kernel.cu:33-38); gamma may be NULL.
+ * Backward-gamma/beta replaces ln_backward_gamma_beta_sm89_kernel<float>
+ *   (kernels/layernorm/ln_backward_gamma_beta_sm89_kernel.cu:15-21). As in the reference the
+ *   result is ADDED to grad_gamma / grad_beta (the reference adds with atomics into
+ *   caller-zeroed buffers); here the sum is formed in a fixed order, so it is deterministic.
+ * The fused backward computes grad_x and adds into grad_gamma / grad_beta in one pass over
+ *   dy and x (no counterpart in the reference, which reads dy and x twice).
+ * ---------------------------------------------------------------------------------------- */
+HK_API hipError_t hk_layer_norm_forward_f32(const float* x, const float* gamma, const float* beta,
+                                     float* y, float* mean_out, float* rstd_out, int rows,
+                                     int cols, float eps, hipStream_t stream);
+HK_API hipError_t hk_ln_backward_input_f32(const float* grad_y, const float* x, const float* mean,
+                                    const float* rstd, const float* gamma, float* grad_x,
+                                    int rows, int cols, hipStream_t stream);
+HK_API hipError_t hk_ln_backward_gamma_beta_f32(const float* grad_y, const float* x, const float* mean,
+                                         const float* rstd, float* grad_gamma, float* grad_beta,
+                                         int rows, int cols, hipStream_t stream);
+HK_API hipError_t hk_layer_norm_backward_f32(const float* grad_y, const float* x, const float* mean,
+                                      const float* rstd, const float* gamma, float* grad_x,
+                                      float* grad_gamma, float* grad_beta, int rows, int cols,
+                                      hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Sparse cross-entropy over fp32 logits [batch_size, vocab_size] with int32 targets.
+ * Forward replaces sparse_ce_forward_kernel_vec_save_stats<float,int32_t>
+ *   (kernels/loss/sparse_ce_forward_kernel_vec_save_stats.cu:14-23): per row
+ *   loss = log(sum) + max - logits[target], and saves max and sum = sum_j exp(x_j - max).
+ * Backward replaces sparseCENormalize_from_stats<float,int32_t>
+ *   (kernels/loss/sparseCENormalize_from_stats.cu:7-17):
+ *   grad = (exp(x - max) / sum - [j == target]) * (*grad_output * host_scale).
+ * Both accept any vocab_size (the reference needs vocab_size % 4 == 0). A target outside
+ * [0, vocab_size) gives a NaN loss and no one-hot term (the reference reads out of bounds).
+ * ---------------------------------------------------------------------------------------- */
+HK_API hipError_t hk_sparse_ce_forward_f32_i32(const float* logits, const int32_t* targets,
+                                        float* losses, float* saved_max, float* saved_sum,
+                                        int64_t batch_size, int64_t vocab_size,
+                                        hipStream_t stream);
+HK_API hipError_t hk_sparse_ce_backward_f32_i32(const float* logits, const int32_t* targets,
+                                         float* grad, const float* saved_max,
+                                         const float* saved_sum, int64_t batch_size,
+                                         int64_t vocab_size, const float* grad_output,
+                                         float host_scale, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Multi-tensor Adam/AdamW, fp32 (decoupled weight decay inside lr * (...)):
+ *   m = fmaf(b1, m, (1-b1) g); v = fmaf(b2, v, (1-b2) g g);
+ *   p = p - lr * ((m / bc1) / (sqrtf(v / bc2) + eps) + wd * p)
+ * hk_multi_tensor_adam keeps the reference's by-value metadata ABI
+ *   (kernels/optimizer/multi_tensor_adam_sm89_kernel.cu:8-27: at most 48 tensors and 320
+ *   chunks of 32768 elements per launch; num_blocks = chunks used).
+ * The plan API has no counterpart in the reference: it stores the tensor/chunk table of any
+ * number of tensors in device memory once, and each step is then one launch.
+ * ---------------------------------------------------------------------------------------- */
+#define HK_ADAM_CHUNK_SIZE 32768
+#define HK_ADAM_MAX_BLOCKS 320
+#define HK_ADAM_MAX_TENSORS 48
+typedef struct hk_adam_launch_metadata {
+  float* params[HK_ADAM_MAX_TENSORS];
+  float* grads[HK_ADAM_MAX_TENSORS];
+  float* ms[HK_ADAM_MAX_TENSORS];
+  float* vs[HK_ADAM_MAX_TENSORS];
+  int64_t sizes[HK_ADAM_MAX_TENSORS];
+  unsigned char block_to_tensor[HK_ADAM_MAX_BLOCKS];
+  int block_to_chunk[HK_ADAM_MAX_BLOCKS];
+} hk_adam_launch_metadata;
+
+HK_API hipError_t hk_multi_tensor_adam(const hk_adam_launch_metadata* meta, int num_blocks, float lr,
+                                float beta1, float beta2, float eps, float weight_decay,
+                                float bias_correction1, float bias_correction2,
+                                hipStream_t stream);
+
+typedef struct hk_adam_plan hk_adam_plan;
+/* params/grads/ms/vs/sizes are HOST arrays of num_tensors device pointers / sizes. */
+HK_API hipError_t hk_adam_plan_create(int num_tensors, float* const* params, float* const* grads,
+                               float* const* ms, float* const* vs, const int64_t* sizes,
+                               hk_adam_plan** plan_out);
+HK_API hipError_t hk_adam_plan_step(const hk_adam_plan* plan, float lr, float beta1, float beta2,
+                             float eps, float weight_decay, float bias_correction1,
+                             float bias_correction2, hipStream_t stream);
+HK_API hipError_t hk_adam_plan_destroy(hk_adam_plan* plan);
+/* Chunks and launches that one step of the plan uses (for reporting). */
+HK_API int64_t hk_adam_plan_num_chunks(const hk_adam_plan* plan);
+
+/* ------------------------------------------------------------------------------------------
+ * Unified sum reduction, fp32 in / fp32 out.
+ * Replaces detail::ReductionLayout + build_reduce_config + launch_reduce_kernel
+ *   (kernels/reduction/unified_reduce_standalone.cu:46-56, 151-221, 702-804).
+ * Paths (same enum order as ReductionLayout::Path):
+ *   HK_REDUCE_INNER   out[o] = sum_k src[o * input_outer_stride + k],  k < reduced_count
+ *                     (input_outer_stride 0 means reduced_count, i.e. contiguous rows)
+ *   HK_REDUCE_OUTER   out[o] = sum_k src[(o / inner_count) * input_outer_stride
+ *                                        + (o % inner_count) + k * input_row_stride]
+ *                     (a leading-axis reduction has num_outputs == inner_count; a middle-axis
+ *                     one has input_outer_stride = the slab stride, as in :393-401)
+ *   HK_REDUCE_GENERIC out[o] = sum_k src[in_offset(k) + out_offset(o)] with the strided
+ *                     offsets given by hk_reduce_generic_f32 (the reference's
+ *                     OffsetCalculator pair, :224-249).
+ * Unlike the reference launcher, no device memory is allocated or freed per call: the
+ * multi-workgroup partials use a workspace the library keeps per device.
+ * ---------------------------------------------------------------------------------------- */
+#define HK_REDUCE_INNER 0
+#define HK_REDUCE_OUTER 1
+#define HK_REDUCE_GENERIC 2
+typedef struct hk_reduction_layout {
+  int32_t path;
+  int64_t num_outputs;
+  int64_t reduced_count;
+  int64_t input_outer_stride;
+  int64_t inner_count;
+  int64_t input_row_stride;
+} hk_reduction_layout;
+
+HK_API hipError_t hk_unified_reduce_sum_f32(const hk_reduction_layout* layout, const float* src,
+                                     float* dst, hipStream_t stream);
+#define HK_REDUCE_MAX_DIMS 10
+HK_API hipError_t hk_reduce_generic_f32(const float* src, float* dst, int out_ndim,
+                                 const int64_t* out_sizes, const int64_t* out_strides,
+                                 int red_ndim, const int64_t* red_sizes,
+                                 const int64_t* red_strides, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HK_H_ */
