@@ -216,13 +216,63 @@ def per_kernel_suite(flush):
     rdst = torch.empty(16384, device=DEV)
     cases.append(("reduce_inner_16384x50304", lambda: hk.unified_reduce_sum(rs, lay, rdst),
                   16384 * 50304 * 4, "hbm"))
+    cases += gemm_cases(g)
     for name, fn, work, bound in cases:
         t = time_kernel(fn, ARGS.reps, flush)
-        ach = work / (t["avg_ms"] * 1e-3) / 1e9
-        out[name] = {"avg_ms": round(t["avg_ms"], 5), "achieved": round(ach, 1), "unit": "GB/s",
-                     "frac": round(ach / W.PEAK_HBM_GBS, 4)}
+        if bound == "hbm":
+            ach = work / (t["avg_ms"] * 1e-3) / 1e9
+            out[name] = {"avg_ms": round(t["avg_ms"], 5), "achieved": round(ach, 1), "unit": "GB/s",
+                         "frac": round(ach / W.PEAK_HBM_GBS, 4)}
+        else:
+            ach = work / (t["avg_ms"] * 1e-3) / 1e12
+            peak = W.PEAK_TFLOPS[bound]
+            out[name] = {"avg_ms": round(t["avg_ms"], 5), "achieved": round(ach, 1),
+                         "unit": "TFLOP/s", "peak": peak, "frac": round(ach / peak, 4)}
         log(name, out[name])
     return out
+
+
+def gemm_cases(g):
+    """BF16 GEMM M=8192 K=1280 N=5120 in NN/NT/TN/TT plus dA (NT) and dB (TN)."""
+    import ctypes
+
+    lib = hk.lib()
+    M, N, K = W.BGEMM["M"], W.BGEMM["N"], W.BGEMM["K"]
+    one = 0x3F80  # bf16 1.0
+    zero = 0
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    A_mk = (torch.randn(M, K, generator=g, device=DEV) * K ** -0.5).to(torch.bfloat16)
+    A_km = A_mk.t().contiguous()
+    B_kn = (torch.randn(K, N, generator=g, device=DEV) * K ** -0.5).to(torch.bfloat16)
+    B_nk = B_kn.t().contiguous()
+    C = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    flop = W.gemm_flop(M, N, K)
+    cases = []
+    for ta, tb in ((0, 0), (0, 1), (1, 0), (1, 1)):
+        a = A_km if ta else A_mk
+        b = B_nk if tb else B_kn
+
+        def run(ta=ta, tb=tb, a=a, b=b):
+            st = lib.hk_bgemm(ta, tb, M, N, K, one, a.data_ptr(), a.shape[1], 0, b.data_ptr(),
+                              b.shape[1], 0, zero, C.data_ptr(), N, 0, 1, stream())
+            assert st == 0
+        cases.append((f"bgemm_{'T' if ta else 'N'}{'T' if tb else 'N'}_8192x5120x1280", run, flop,
+                      "bf16"))
+    # backward of Y[M,N] = X[M,K] W[K,N]: dX = dY W^T (NT, [M,N]x[N,K]); dW = X^T dY (TN)
+    dY = (torch.randn(M, N, generator=g, device=DEV) * N ** -0.5).to(torch.bfloat16)
+    dX = torch.empty(M, K, device=DEV, dtype=torch.bfloat16)
+    dW = torch.empty(K, N, device=DEV, dtype=torch.bfloat16)
+
+    def run_da():
+        assert lib.hk_bgemm_nt_backward(M, K, N, one, dY.data_ptr(), N, 0, B_kn.data_ptr(), N, 0,
+                                        zero, dX.data_ptr(), K, 0, 1, stream()) == 0
+
+    def run_db():
+        assert lib.hk_bgemm_tn_backward(K, N, M, one, A_mk.data_ptr(), K, 0, dY.data_ptr(), N, 0,
+                                        zero, dW.data_ptr(), N, 0, 1, stream()) == 0
+    cases.append(("bgemm_dA_NT_8192x1280x5120", run_da, flop, "bf16"))
+    cases.append(("bgemm_dB_TN_1280x5120x8192", run_db, flop, "bf16"))
+    return cases
 
 
 def main():

@@ -6,7 +6,7 @@ the reference kernel surface over torch device tensors (``hyperkernels_amd.kerne
 """
 from __future__ import annotations
 
-__all__ = ["kernels", "lib"]
+__all__ = ["lib"]
 
 
 def lib():
@@ -14,11 +14,3 @@ def lib():
     from ._lib import lib as _load
 
     return _load()
-
-
-def __getattr__(name):
-    if name == "kernels":
-        from . import kernels
-
-        return kernels
-    raise AttributeError(name)

@@ -25,6 +25,7 @@ _C_TYPES = {
     "int": ctypes.c_int,
     "int32_t": ctypes.c_int32,
     "int64_t": ctypes.c_int64,
+    "long long": ctypes.c_longlong,
     "float": ctypes.c_float,
     "hk_bf16": ctypes.c_uint16,
     "hipError_t": ctypes.c_int,

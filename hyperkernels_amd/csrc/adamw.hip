@@ -13,11 +13,11 @@
 //   - hk_multi_tensor_adam: the reference's by-value launch metadata (<= 48 tensors,
 //     <= 320 chunks of 32768 elements per launch).
 //   - the plan API: the tensor table and chunk table of any number of tensors live in device
-//     memory, built once, so a whole-model step (GPT-2 small: 148 tensors, 3,892 chunks) is a
-//     single launch with no host-to-device traffic.
+//     memory, built once, so a whole-model step (GPT-2 small: 148 tensors, 30,450 chunks of
+//     4096 elements) is a single launch with no host-to-device traffic.
 // Each workgroup streams one chunk: a scalar head up to the first 16-byte boundary, 16-byte
-// loads of p, g, m, v in the body (two iterations in flight per lane), and a scalar tail. A
-// tensor whose four arrays do not share the same 16-byte phase is processed scalar.
+// loads of p, g, m, v in the body (four vectors of each in flight per lane), and a scalar
+// tail. A tensor whose four arrays do not share the same 16-byte phase is processed scalar.
 #include <vector>
 
 #include "hk_device.h"
@@ -26,6 +26,10 @@
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+// Elements per workgroup in the plan's chunk table: one pass of kUnroll 16-byte vectors per
+// lane, so each workgroup is short-lived and the device keeps many of them in flight.
+constexpr int kPlanChunk = kThreads * kUnroll * 4;
 
 struct AdamHyper {
   float lr, beta1, beta2, eps, wd, bc1, bc2;
@@ -80,20 +84,29 @@ __device__ __forceinline__ void adam_chunk(float* __restrict__ p, const float* _
   float4* m4 = reinterpret_cast<float4*>(m + vs);
   float4* v4 = reinterpret_cast<float4*>(v + vs);
   const int64_t nv = (ve - vs) >> 2;
-  int64_t i = threadIdx.x;
-  for (; i + kThreads < nv; i += 2 * kThreads) {
-    float4 pa = p4[i], ga = hk::ld_nt(g4 + i), ma = m4[i], va = v4[i];
-    float4 pb = p4[i + kThreads], gb = hk::ld_nt(g4 + i + kThreads),
-           mb = m4[i + kThreads], vb = v4[i + kThreads];
-    adam_update4(pa, ga, ma, va, h);
-    adam_update4(pb, gb, mb, vb, h);
-    p4[i] = pa; m4[i] = ma; v4[i] = va;
-    p4[i + kThreads] = pb; m4[i + kThreads] = mb; v4[i + kThreads] = vb;
-  }
-  for (; i < nv; i += kThreads) {
-    float4 pa = p4[i], ga = g4[i], ma = m4[i], va = v4[i];
-    adam_update4(pa, ga, ma, va, h);
-    p4[i] = pa; m4[i] = ma; v4[i] = va;
+  // kUnroll vectors of each of p, g, m, v per lane per pass, all loads issued before any math
+  for (int64_t i = threadIdx.x; i < nv; i += kUnroll * kThreads) {
+    float4 pa[kUnroll], ga[kUnroll], ma[kUnroll], va[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t k = i + u * kThreads;
+      if (k < nv) {
+        pa[u] = p4[k];
+        ga[u] = hk::ld_nt(g4 + k);
+        ma[u] = m4[k];
+        va[u] = v4[k];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t k = i + u * kThreads;
+      if (k < nv) {
+        adam_update4(pa[u], ga[u], ma[u], va[u], h);
+        p4[k] = pa[u];
+        m4[k] = ma[u];
+        v4[k] = va[u];
+      }
+    }
   }
   for (int64_t j = ve + threadIdx.x; j < end; j += kThreads) {
     float pj = p[j], mj = m[j], vj = v[j];
@@ -134,8 +147,8 @@ __global__ __launch_bounds__(kThreads) void adam_plan_kernel(const TensorEntry* 
                                                              AdamHyper h) {
   const ChunkEntry c = chunks[blockIdx.x];
   const TensorEntry t = tensors[c.tensor];
-  const int64_t start = static_cast<int64_t>(c.chunk) * HK_ADAM_CHUNK_SIZE;
-  int64_t end = start + HK_ADAM_CHUNK_SIZE;
+  const int64_t start = static_cast<int64_t>(c.chunk) * kPlanChunk;
+  int64_t end = start + kPlanChunk;
   if (end > t.numel) end = t.numel;
   if (start >= end) return;
   adam_chunk(t.p, t.g, t.m, t.v, start, end, h);
@@ -176,7 +189,7 @@ extern "C" hipError_t hk_adam_plan_create(int num_tensors, float* const* params,
   for (int t = 0; t < num_tensors; ++t) {
     HK_CHECK_ARG(sizes[t] >= 0);
     HK_CHECK_ARG(sizes[t] == 0 || (params[t] && grads[t] && ms[t] && vs[t]));
-    const int64_t nch = hk::ceil_div(sizes[t], HK_ADAM_CHUNK_SIZE);
+    const int64_t nch = hk::ceil_div(sizes[t], kPlanChunk);
     HK_CHECK_ARG(nch <= INT32_MAX);
     tensors[t] = TensorEntry{params[t], grads[t], ms[t], vs[t], sizes[t]};
     for (int64_t c = 0; c < nch; ++c) chunks.push_back(ChunkEntry{t, static_cast<int32_t>(c)});

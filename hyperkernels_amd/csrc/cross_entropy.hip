@@ -100,13 +100,20 @@ __device__ __forceinline__ float ce_grad1(float v, float mx, float inv_sum, floa
   return (__expf(v - mx) * inv_sum - (hit ? 1.0f : 0.0f)) * scale;
 }
 
-// Vector path: logits and grad share the same 16-byte phase on every row.
+// Vector path: logits and grad share the same 16-byte phase on every row. The row's body is cut
+// into chunks of kChunkVec 16-byte vectors, one workgroup each (grid = rows x chunks), and each
+// lane issues all of its kUnroll loads before computing: a short-lived workgroup with its
+// loads in flight keeps more bytes moving than one long loop per row. Chunk 0 also writes the
+// row's head, the last chunk its tail.
+constexpr int kChunkVec = kThreads * kUnroll;
+
 __global__ __launch_bounds__(kThreads) void ce_backward(
     const float* __restrict__ logits, const int32_t* __restrict__ targets,
     float* __restrict__ grad, const float* __restrict__ saved_max,
-    const float* __restrict__ saved_sum, int64_t vocab, const float* __restrict__ grad_output,
-    float host_scale) {
-  const int64_t row = blockIdx.x;
+    const float* __restrict__ saved_sum, int64_t vocab, int nchunks,
+    const float* __restrict__ grad_output, float host_scale) {
+  const int64_t row = blockIdx.x / nchunks;
+  const int chunk = blockIdx.x - static_cast<int>(row) * nchunks;
   const float* x = logits + row * vocab;
   float* g = grad + row * vocab;
   const int tid = threadIdx.x;
@@ -117,38 +124,36 @@ __global__ __launch_bounds__(kThreads) void ce_backward(
 
   int64_t h, nb;
   split_row(x, vocab, h, nb);
-  if (tid < h) g[tid] = ce_grad1(x[tid], mx, inv_sum, scale, tid == t);
+  if (chunk == 0 && tid < h) g[tid] = ce_grad1(x[tid], mx, inv_sum, scale, tid == t);
+  if (chunk == nchunks - 1) {
+    const int64_t j = h + 4 * nb + tid;
+    if (j < vocab) g[j] = ce_grad1(x[j], mx, inv_sum, scale, j == t);
+  }
   const float4* xb = reinterpret_cast<const float4*>(x + h);
   float4* gb = reinterpret_cast<float4*>(g + h);
-  const int64_t tb = t - h;  // target position relative to the body start
-  int64_t i = tid;
-  for (; i + (kUnroll - 1) * kThreads < nb; i += kUnroll * kThreads) {
-    float4 v[kUnroll];
+  // target position relative to this chunk's first element (32-bit: a chunk is 4096 values)
+  const int64_t base = static_cast<int64_t>(chunk) * kChunkVec;
+  const int64_t trel64 = t - h - 4 * base;
+  const int trel = (trel64 >= 0 && trel64 < 4 * kChunkVec) ? static_cast<int>(trel64) : -1;
+  float4 v[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) v[u] = hk::ld_nt(xb + i + u * kThreads);
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + tid + u * kThreads;
+    if (i < nb) v[u] = hk::ld_nt(xb + i);
+  }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t j = 4 * (i + u * kThreads);
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + tid + u * kThreads;
+    if (i < nb) {
+      const int j = 4 * (tid + u * kThreads);
       float4 o;
-      o.x = ce_grad1(v[u].x, mx, inv_sum, scale, j + 0 == tb);
-      o.y = ce_grad1(v[u].y, mx, inv_sum, scale, j + 1 == tb);
-      o.z = ce_grad1(v[u].z, mx, inv_sum, scale, j + 2 == tb);
-      o.w = ce_grad1(v[u].w, mx, inv_sum, scale, j + 3 == tb);
-      hk::st_nt(gb + i + u * kThreads, o);
+      o.x = ce_grad1(v[u].x, mx, inv_sum, scale, j + 0 == trel);
+      o.y = ce_grad1(v[u].y, mx, inv_sum, scale, j + 1 == trel);
+      o.z = ce_grad1(v[u].z, mx, inv_sum, scale, j + 2 == trel);
+      o.w = ce_grad1(v[u].w, mx, inv_sum, scale, j + 3 == trel);
+      hk::st_nt(gb + i, o);
     }
   }
-  for (; i < nb; i += kThreads) {
-    const float4 v = hk::ld_nt(xb + i);
-    const int64_t j = 4 * i;
-    float4 o;
-    o.x = ce_grad1(v.x, mx, inv_sum, scale, j + 0 == tb);
-    o.y = ce_grad1(v.y, mx, inv_sum, scale, j + 1 == tb);
-    o.z = ce_grad1(v.z, mx, inv_sum, scale, j + 2 == tb);
-    o.w = ce_grad1(v.w, mx, inv_sum, scale, j + 3 == tb);
-    hk::st_nt(gb + i, o);
-  }
-  for (int64_t j = h + 4 * nb + tid; j < vocab; j += kThreads)
-    g[j] = ce_grad1(x[j], mx, inv_sum, scale, j == t);
 }
 
 // Scalar path for a grad buffer whose 16-byte phase differs from the logits buffer's.
@@ -192,8 +197,17 @@ extern "C" hipError_t hk_sparse_ce_backward_f32_i32(const float* logits, const i
   HK_CHECK_ARG(logits && targets && grad && saved_max && saved_sum);
   const bool same_phase = ((reinterpret_cast<uintptr_t>(logits) ^
                             reinterpret_cast<uintptr_t>(grad)) & 15u) == 0;
-  hipLaunchKernelGGL(same_phase ? ce_backward : ce_backward_scalar,
-                     dim3(static_cast<unsigned>(batch_size)), dim3(kThreads), 0, stream, logits,
-                     targets, grad, saved_max, saved_sum, vocab_size, grad_output, host_scale);
+  if (!same_phase) {
+    hipLaunchKernelGGL(ce_backward_scalar, dim3(static_cast<unsigned>(batch_size)), dim3(kThreads),
+                       0, stream, logits, targets, grad, saved_max, saved_sum, vocab_size,
+                       grad_output, host_scale);
+    return hk::launch_status();
+  }
+  // body vectors per row are at most vocab / 4; at least one chunk per row (head/tail only)
+  const int64_t nchunks = hk::ceil_div(vocab_size / 4 + 1, kChunkVec);
+  HK_CHECK_ARG(nchunks <= INT32_MAX && batch_size * nchunks <= INT32_MAX);
+  hipLaunchKernelGGL(ce_backward, dim3(static_cast<unsigned>(batch_size * nchunks)),
+                     dim3(kThreads), 0, stream, logits, targets, grad, saved_max, saved_sum,
+                     vocab_size, static_cast<int>(nchunks), grad_output, host_scale);
   return hk::launch_status();
 }

@@ -2,9 +2,9 @@
 //
 // Reference behaviour: kernels/gelu/gelu_forward_sm89_kernel.cu:19-22 (forward formula) and
 // kernels/gelu/gelu_backward_sm89_kernel.cu:24-30 (analytic derivative). The reference uses the
-// PTX tanh.approx instruction; this file evaluates tanh from the exponential,
-// tanh(u) = 1 - 2 / (exp(2u) + 1), whose absolute error stays near 1e-7 over the whole range
-// (the formula only enters as 1 + tanh and 1 - tanh^2, so absolute error is what matters).
+// PTX tanh.approx instruction; this file never forms tanh itself: the formula only needs
+// 1 + tanh(u) and 1 - tanh(u)^2, which are evaluated through the logistic function
+// (1 + tanh(u)) / 2 = 1 / (1 + exp(-2u)) with relative error of a few ulp everywhere.
 //
 // HBM layout: flat contiguous tensors. Each lane moves 16 bytes per access (8 bf16 or
 // 4 fp32) and a workgroup of 256 lanes covers UNROLL consecutive 4 KiB spans, so every wave
@@ -19,22 +19,27 @@ constexpr float kGeluCoef = 0.044715f;               // Hendrycks & Gimpel tanh 
 constexpr int kThreads = 256;
 constexpr int kUnroll = 4;
 
-__device__ __forceinline__ float tanh_from_exp(float u) {
-  const float e = __expf(2.0f * u);
-  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+// (1 + tanh(u)) / 2 = sigmoid(2u) = 1 / (1 + exp(-2u)): no cancellation for u << 0, where
+// 1 + tanh(u) formed from a rounded tanh loses most of its digits. exp overflow (u << 0) gives
+// s = 0 and exp underflow (u >> 0) gives s = 1, the correct limits.
+__device__ __forceinline__ float half_one_plus_tanh(float u) {
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * u));
 }
 
+// GELU(x) = 0.5 x (1 + tanh(u)) = x s
 __device__ __forceinline__ float gelu_fwd(float x) {
   const float u = kSqrt2OverPi * (x + kGeluCoef * x * x * x);
-  return 0.5f * x * (1.0f + tanh_from_exp(u));
+  return x * half_one_plus_tanh(u);
 }
 
+// GELU'(x) = 0.5 (1 + th) + 0.5 x (1 - th^2) du = s + 2 x s (1 - s) du, with s as above
+// (1 - th^2 = (1 - th)(1 + th) = 4 s (1 - s)).
 __device__ __forceinline__ float gelu_grad(float x) {
   const float x2 = x * x;
   const float u = kSqrt2OverPi * (x + kGeluCoef * x2 * x);
   const float du = kSqrt2OverPi * (1.0f + 3.0f * kGeluCoef * x2);
-  const float th = tanh_from_exp(u);
-  return 0.5f * (1.0f + th) + 0.5f * x * (1.0f - th * th) * du;
+  const float s = half_one_plus_tanh(u);
+  return s + 2.0f * x * (s * (1.0f - s)) * du;
 }
 
 // Element access for the two storage types.

@@ -89,12 +89,17 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_reg(const float4* __restrict_
 // ------------------------------------------------------------------------------------------
 // Backward, register-resident rows. WRITE_DX: produce grad_x. DO_GB: accumulate the
 // per-workgroup gamma/beta partials into part[blockIdx.x][2 * cols] (gamma then beta).
+// Each wave walks its rows with the next row's dy / x already in flight (software prefetch),
+// so the two wave reductions of one row overlap the loads of the next.
 // ------------------------------------------------------------------------------------------
 template <int VPL, bool WRITE_DX, bool DO_GB>
 __global__ __launch_bounds__(kThreads) void ln_bwd_reg(
     const float4* __restrict__ dy, const float4* __restrict__ x, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float4* __restrict__ gamma, float4* __restrict__ dx,
     float* __restrict__ part, int rows, int cols4, float inv_cols) {
+  // Every product below is rounded on its own (as the reference formula is written), so a
+  // row whose terms cancel exactly (cols == 1) gives exactly zero.
+#pragma clang fp contract(off)
   extern __shared__ float4 lds4[];  // [kWavesPerBlock][2][cols4] when DO_GB
   const int lane = threadIdx.x & (HK_WAVE - 1);
   const int wave = threadIdx.x >> 6;
@@ -107,23 +112,38 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_reg(
     acc_g[i] = f4_zero();
     acc_b[i] = f4_zero();
   }
-  for (int row = blockIdx.x * kWavesPerBlock + wave; row < rows;
-       row += gridDim.x * kWavesPerBlock) {
-    const float m = mean[row], rs = rstd[row];
-    const float4* dyr = dy + static_cast<int64_t>(row) * cols4;
-    const float4* xr = x + static_cast<int64_t>(row) * cols4;
-    float4 d[VPL], n[VPL];
+  const int stride = gridDim.x * kWavesPerBlock;
+  int row = blockIdx.x * kWavesPerBlock + wave;
+  float4 dn[VPL], xn[VPL];
+  float mn = 0.f, rn = 0.f;
+  auto fetch = [&](int r) {
+    const float4* dyr = dy + static_cast<int64_t>(r) * cols4;
+    const float4* xr = x + static_cast<int64_t>(r) * cols4;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int c = lane + i * HK_WAVE;
-      d[i] = (c < cols4) ? hk::ld_nt(dyr + c) : f4_zero();
-      n[i] = (c < cols4) ? hk::ld_nt(xr + c) : make_float4(m, m, m, m);
+      dn[i] = (c < cols4) ? hk::ld_nt(dyr + c) : f4_zero();
+      xn[i] = (c < cols4) ? hk::ld_nt(xr + c) : f4_zero();
     }
+    mn = mean[r];
+    rn = rstd[r];
+  };
+  if (row < rows) fetch(row);
+  for (; row < rows; row += stride) {
+    float4 d[VPL], n[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      d[i] = dn[i];
+      n[i] = xn[i];
+    }
+    const float m = mn, rs = rn;
+    if (row + stride < rows) fetch(row + stride);
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      n[i].x = (n[i].x - m) * rs; n[i].y = (n[i].y - m) * rs;
-      n[i].z = (n[i].z - m) * rs; n[i].w = (n[i].w - m) * rs;
+      const bool in = lane + i * HK_WAVE < cols4;
+      n[i].x = in ? (n[i].x - m) * rs : 0.f; n[i].y = in ? (n[i].y - m) * rs : 0.f;
+      n[i].z = in ? (n[i].z - m) * rs : 0.f; n[i].w = in ? (n[i].w - m) * rs : 0.f;
       if (DO_GB) {
         acc_g[i].x += d[i].x * n[i].x; acc_g[i].y += d[i].y * n[i].y;
         acc_g[i].z += d[i].z * n[i].z; acc_g[i].w += d[i].w * n[i].w;
@@ -177,20 +197,38 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_reg(
   }
 }
 
-// Sums nparts partials [nparts][2 * cols] in part order and adds them into grad_gamma /
-// grad_beta. One thread per output column.
-__global__ __launch_bounds__(kThreads) void ln_gb_finalize(const float* __restrict__ part,
-                                                           int nparts, int cols,
-                                                           float* __restrict__ grad_gamma,
-                                                           float* __restrict__ grad_beta) {
-  const int c = blockIdx.x * kThreads + threadIdx.x;
-  if (c >= 2 * cols) return;
-  float s = 0.f;
-  for (int p = 0; p < nparts; ++p) s += part[static_cast<int64_t>(p) * 2 * cols + c];
-  if (c < cols) {
-    if (grad_gamma) grad_gamma[c] += s;
-  } else {
-    if (grad_beta) grad_beta[c - cols] += s;
+// Sums nparts partials [nparts][2 * cols] in a fixed order and adds them into grad_gamma /
+// grad_beta. A workgroup of 16 waves owns 64 columns: wave w sums partials w, w + 16, ...
+// (eight loads in flight per lane), then the 16 wave sums are added in wave order in LDS.
+constexpr int kFinWaves = 16;
+__global__ __launch_bounds__(kFinWaves * HK_WAVE) void ln_gb_finalize(
+    const float* __restrict__ part, int nparts, int cols, float* __restrict__ grad_gamma,
+    float* __restrict__ grad_beta) {
+  __shared__ float red[kFinWaves][HK_WAVE];
+  const int lane = threadIdx.x & (HK_WAVE - 1);
+  const int wave = threadIdx.x >> 6;
+  const int c = blockIdx.x * HK_WAVE + lane;
+  const int width = 2 * cols;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (c < width) {
+    int p = wave;
+    for (; p + 7 * kFinWaves < nparts; p += 8 * kFinWaves) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[u] += part[static_cast<int64_t>(p + u * kFinWaves) * width + c];
+    }
+    for (; p < nparts; p += kFinWaves) acc[0] += part[static_cast<int64_t>(p) * width + c];
+  }
+  red[wave][lane] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  __syncthreads();
+  if (wave == 0 && c < width) {
+    float s = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < kFinWaves; ++w) s += red[w][lane];
+    if (c < cols) {
+      if (grad_gamma) grad_gamma[c] += s;
+    } else {
+      if (grad_beta) grad_beta[c - cols] += s;
+    }
   }
 }
 
@@ -244,6 +282,7 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_input_rowblock(
     const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ gamma, float* __restrict__ dx,
     int cols) {
+#pragma clang fp contract(off)
   __shared__ float red[kWavesPerBlock];
   const int64_t row = blockIdx.x;
   const float m = mean[row], rs = rstd[row];
@@ -358,8 +397,8 @@ hipError_t launch_bwd(const float* dy, const float* x, const float* mean, const 
       return hk::launch_status();
     }));
     if (do_gb) {
-      hipLaunchKernelGGL(ln_gb_finalize, dim3(static_cast<unsigned>(hk::ceil_div(2 * cols, kThreads))),
-                         dim3(kThreads), 0, stream, part, grid, cols, dgamma, dbeta);
+      hipLaunchKernelGGL(ln_gb_finalize, dim3(static_cast<unsigned>(hk::ceil_div(2 * cols, HK_WAVE))),
+                         dim3(kFinWaves * HK_WAVE), 0, stream, part, grid, cols, dgamma, dbeta);
       HK_RETURN_IF_ERROR(hk::launch_status());
     }
     return hipSuccess;

@@ -188,6 +188,45 @@ HK_API hipError_t hk_reduce_generic_f32(const float* src, float* dst, int out_nd
                                  int red_ndim, const int64_t* red_sizes,
                                  const int64_t* red_strides, hipStream_t stream);
 
+/* ------------------------------------------------------------------------------------------
+ * BF16 batched GEMM: C = alpha * op(A) op(B) + beta * C, bf16 in/out, fp32 accumulation,
+ * row-major. op(A) = A [M,K] (lda >= K) or, transposed, A stored [K,M] (lda >= M);
+ * op(B) = B [K,N] (ldb >= N) or, transposed, B stored [N,K] (ldb >= K). alpha/beta are bf16
+ * bit patterns, applied in fp32 with one final rounding to bf16.
+ * hk_bgemm replaces bgemm_NN_kernel<transA, transB> (NN/NT/TN/TT;
+ *   blas/bf16/bgemm_nn_128x128_sm89_kernel.cu:23-32, trans = mycublasOperation_t: 0 = N,
+ *   1 = T, 2 = C treated as T) and bgemm_NN_128x128_64x3_kernel (…_64x3_sm89_kernel.cu:23).
+ * hk_bgemm_core replaces bgemm_backward_template_kernel<Cfg, Aligned, SplitK, Layout>
+ *   (blas/bf16/bgemm_core_template.cu:61-70); layout is HK_LAYOUT_{NT,TN,NN} (the reference's
+ *   BgemmLayout order, :59). splitK > 1 sums fp32 partials in split order (the reference adds
+ *   bf16 atomics), so the result does not depend on splitK beyond fp32 rounding.
+ * hk_bgemm_nt_backward (dA = dY * B^T) replaces bgemm_nt_backward_kernel
+ *   (blas/bf16/bgemm_backward_nt_sm89_kernel.cu:23-32); hk_bgemm_tn_backward (dB = A^T * dY)
+ *   replaces bgemm_tn_backward_kernel (blas/bf16/bgemm_backward_tn_sm89_kernel.cu:25-34).
+ * Any M, N, K; the MFMA path needs the contiguous extents, leading dimensions and strides to
+ * be multiples of 8 and 16-byte aligned pointers (the reference's own precondition,
+ * bgemm_test.cu:252-256); other shapes run on a slower fp32-accumulating kernel.
+ * ---------------------------------------------------------------------------------------- */
+#define HK_LAYOUT_NT 0
+#define HK_LAYOUT_TN 1
+#define HK_LAYOUT_NN 2
+HK_API hipError_t hk_bgemm(int transA, int transB, int M, int N, int K, hk_bf16 alpha,
+                           const hk_bf16* A, int lda, long long strideA, const hk_bf16* B,
+                           int ldb, long long strideB, hk_bf16 beta, hk_bf16* C, int ldc,
+                           long long strideC, int batchCount, hipStream_t stream);
+HK_API hipError_t hk_bgemm_core(int layout, int splitK, int M, int N, int K, hk_bf16 alpha,
+                                const hk_bf16* A, int lda, long long strideA, const hk_bf16* B,
+                                int ldb, long long strideB, hk_bf16 beta, hk_bf16* C, int ldc,
+                                long long strideC, int batchCount, hipStream_t stream);
+HK_API hipError_t hk_bgemm_nt_backward(int M, int N, int K, hk_bf16 alpha, const hk_bf16* A,
+                                       int lda, long long strideA, const hk_bf16* B, int ldb,
+                                       long long strideB, hk_bf16 beta, hk_bf16* C, int ldc,
+                                       long long strideC, int batchCount, hipStream_t stream);
+HK_API hipError_t hk_bgemm_tn_backward(int M, int N, int K, hk_bf16 alpha, const hk_bf16* A,
+                                       int lda, long long strideA, const hk_bf16* B, int ldb,
+                                       long long strideB, hk_bf16 beta, hk_bf16* C, int ldc,
+                                       long long strideC, int batchCount, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,6 +20,15 @@ def L():
     return _lib.lib()
 
 
+def test_package_front_end_imports():
+    import hyperkernels_amd
+    from hyperkernels_amd import kernels, workloads
+
+    assert callable(kernels.gelu_forward) and callable(kernels.AdamPlan)
+    assert workloads.GPT2_NUM_PARAMS == 124_439_808
+    assert hyperkernels_amd.lib() is not None
+
+
 def test_every_header_symbol_is_exported(L):
     from hyperkernels_amd import _lib
 
