@@ -272,6 +272,19 @@ def gemm_cases(g):
                                         zero, dW.data_ptr(), N, 0, 1, stream()) == 0
     cases.append(("bgemm_dA_NT_8192x1280x5120", run_da, flop, "bf16"))
     cases.append(("bgemm_dB_TN_1280x5120x8192", run_db, flop, "bf16"))
+    # FP32 SGEMM 4096^3, split-K 4, fused bias (added once), NN
+    S = W.SGEMM
+    sa = torch.randn(S["M"], S["K"], generator=g, device=DEV) * S["K"] ** -0.5
+    sb = torch.randn(S["K"], S["N"], generator=g, device=DEV) * S["K"] ** -0.5
+    sbias = torch.randn(S["N"], generator=g, device=DEV) * 0.02
+    sc = torch.empty(S["M"], S["N"], device=DEV)
+
+    def run_sgemm():
+        assert lib.hk_sgemm(2, S["M"], S["N"], S["K"], 1.0, sa.data_ptr(), S["K"], 0,
+                            sb.data_ptr(), S["N"], 0, 0.0, sc.data_ptr(), S["N"], 0,
+                            sbias.data_ptr(), S["N"], 1, S["split_k"], stream()) == 0
+    cases.append(("sgemm_NN_4096^3_splitk4_bias", run_sgemm,
+                  W.gemm_flop(S["M"], S["N"], S["K"]), "fp32_matrix"))
     return cases
 
 

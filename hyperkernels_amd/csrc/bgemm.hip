@@ -16,8 +16,8 @@
 //     128 x 128 block of C as 4 x 4 tiles of v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators
 //     per lane). Per 16-deep k step a wave issues 16 MFMAs against 8 LDS fragment reads.
 //   - Both operands live in LDS "k-contiguous" ([row][64 k] bf16, 128 B rows; chunk
-//     placement permuted over row pairs so fragment reads and both store patterns are free of
-//     bank conflicts, see lds_off). An operand that is k-contiguous in HBM is copied as
+//     placement XOR-permuted so fragment reads and both store patterns are free of bank
+//     conflicts, see lds_off). An operand that is k-contiguous in HBM is copied as
 //     16-byte chunks; one that is M- or N-contiguous (A^T, plain B) is read as 8 x 8 bf16
 //     blocks along its contiguous axis and transposed in registers before the LDS store, so
 //     all four layouts share one compute loop and every HBM access is a 16-byte load.
@@ -52,19 +52,17 @@ constexpr size_t kLdsBytes = kLdsMain > kLdsEpi ? kLdsMain : kLdsEpi;
 typedef short bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-// LDS layout of one operand stage: 256 rows x 64 k (bf16), 128-byte rows, taken in pairs of rows
-// (256 bytes = all 64 banks) whose 16 chunks of 16 bytes are permuted by
-// slot = ((row & 1) * 8 + chunk) ^ h(row / 2), h(p) = (p ^ (p >> 2)) & 15.
-// With that permutation the three access patterns below touch 16 distinct chunk slots (all 64
-// banks) in every group of 16 lanes:
-//   - MFMA fragment reads: 16 consecutive rows, one chunk;
-//   - k-major stores: two adjacent rows, 8 chunks each;
-//   - transposed stores: rows 8l + j for 16 consecutive l, one chunk.
+// LDS layout of one operand stage: 256 rows x 64 k (bf16). A row is 128 bytes, i.e. one pass
+// over the 32 LDS banks; its eight 16-byte chunks are placed at chunk ^ f(row),
+// f(row) = (row ^ (row >> 3)) & 7. A 16-byte LDS access is served 8 lanes at a time, and with
+// this placement each group of 8 lanes touches 8 distinct chunk positions (all 32 banks) in the
+// three access patterns below:
+//   - MFMA fragment reads: 8 consecutive rows, one chunk (f = row ^ const);
+//   - k-major stores: one row, 8 chunks;
+//   - transposed stores: rows 8l + j for 8 consecutive l, one chunk (f = j ^ l).
 // Returns the offset in bf16 elements.
 __device__ __forceinline__ int lds_off(int row, int chunk) {
-  const int p = row >> 1;
-  const int slot = (((row & 1) << 3) | chunk) ^ ((p ^ (p >> 2)) & 15);
-  return (p * 16 + slot) * 8;
+  return row * 64 + ((chunk ^ ((row ^ (row >> 3)) & 7)) * 8);
 }
 
 // Transposes an 8 x 8 block of bf16: in[r] holds 8 values of row r (two per 32-bit word, lower

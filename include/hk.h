@@ -227,6 +227,42 @@ HK_API hipError_t hk_bgemm_tn_backward(int M, int N, int K, hk_bf16 alpha, const
                                        long long strideB, hk_bf16 beta, hk_bf16* C, int ldc,
                                        long long strideC, int batchCount, hipStream_t stream);
 
+/* ------------------------------------------------------------------------------------------
+ * FP32 batched GEMM on fp32 MFMA (full fp32 products; the reference uses single-pass TF32),
+ * row-major, layout HK_LAYOUT_{NT,TN,NN} as SgemmLayout (blas/fp32/sgemm_sm89_core_template.cu:9).
+ * hk_sgemm replaces sgemm_sm89_kernel<Cfg, Aligned, SplitK, Layout> (…core_template.cu:85-94):
+ *   C = alpha * op(A) op(B) + beta * C + bias, the bias added EXACTLY ONCE whatever splitK is
+ *   (the reference's split-K path adds it once per split). bias may be NULL; otherwise
+ *   bias_stride selects it as in the reference (:303-315): N -> bias[col];
+ *   M*N -> bias[(batch % M) * N + col]; 1 -> bias[0]; any other value is rejected.
+ *   splitK >= 1 (the reference's split-K pre-scale kernel sgemm_sm89_scale_kernel, :329-333, is
+ *   folded in: no caller pre-pass is needed).
+ * hk_sgemm_addmm replaces sgemm_addmm_sm89_kernel (blas/fp32/sgemm_addmm_sm89_kernel.cu:66-76):
+ *   NN, C = alpha * A B + beta * C + beta * bias, bias_numel in {1, N, M*N} as there.
+ * hk_sgemm_layout replaces every tile-specialised SGEMM kernel (sgemm_nn_256x128_sm89_2_opt_k,
+ *   sgemm_nn_256x64_sm89_2_k, sgemm_nn_64x64_sm89_2_k, sgemm_nn_256x128_bypass_sm89_batched_kernel,
+ *   sgemm_nt_{256x128,128x128,64x128}_sm89_2_k, sgemm_tn_256x128_sm89_optimized,
+ *   sgemm_tn_{128x128,256x64}_sm89_2_k, sgemm_tn_{64x64,32x32}_sm89_k): the same product
+ *   C = alpha * op(A) op(B) + beta * C for the kernel's layout (pass splitK = 1 for kernels
+ *   without a splitK argument). The tile shape is the library's choice.
+ * Any M, N, K; the MFMA path needs the contiguous extents, leading dimensions and strides to
+ * be multiples of 4 and 16-byte aligned pointers (sgemm_test.cu:240-243); other shapes run on a
+ * slower k-order kernel.
+ * ---------------------------------------------------------------------------------------- */
+HK_API hipError_t hk_sgemm(int layout, int M, int N, int K, float alpha, const float* A, int lda,
+                           long long strideA, const float* B, int ldb, long long strideB,
+                           float beta, float* C, int ldc, long long strideC, const float* bias,
+                           long long bias_stride, int batchCount, int splitK, hipStream_t stream);
+HK_API hipError_t hk_sgemm_addmm(int M, int N, int K, float alpha, const float* A, int lda,
+                                 long long strideA, const float* B, int ldb, long long strideB,
+                                 float beta, const float* bias, int64_t bias_numel, float* C,
+                                 int ldc, long long strideC, int batchCount, hipStream_t stream);
+HK_API hipError_t hk_sgemm_layout(int layout, int M, int N, int K, float alpha, const float* A,
+                                  int lda, long long strideA, const float* B, int ldb,
+                                  long long strideB, float beta, float* C, int ldc,
+                                  long long strideC, int batchCount, int splitK,
+                                  hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

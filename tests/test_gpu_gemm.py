@@ -150,3 +150,140 @@ def test_bgemm_baseline_shape_sampled_rows(hk, orc, ta, tb):
     rel = max_rel(orc.bf16_to_f32(out[rows]), ref)
     print(f"baseline rel {rel:.2e}")
     assert rel <= 1e-2
+
+
+# ---------------------------------------------------------------------------------------------
+# FP32 SGEMM (blas/fp32): C = alpha op(A) op(B) + beta C + bias, bias added once; fp32 MFMA.
+# Tolerance: BASELINE.json's 2e-3 relative (max|err| / max|ref|) against the oracle's fp32
+# k-order reference (sgemm_test.cu:176-185 restated on the CPU).
+# ---------------------------------------------------------------------------------------------
+SG_LAYOUT = {"NT": (0, 0, 1), "TN": (1, 1, 0), "NN": (2, 0, 0)}  # name -> (enum, ta, tb)
+SG_HARNESS = [(256, 256, 256), (512, 384, 128), (256, 128, 96)]  # sgemm_test.cu:245
+
+
+def _sg_operands(orc, M, N, K, ta, tb, seed, normal=False):
+    if normal:  # A, B ~ N(0, 1/sqrt(K)), bias ~ N(0, 0.02), C0 ~ N(0, 1)
+        a = orc.normal(M * K, seed, 0.0, K ** -0.5)
+        b = orc.normal(K * N, seed + 1, 0.0, K ** -0.5)
+        c0 = orc.normal(M * N, seed + 2)
+        bias = orc.normal(N, seed + 3, 0.0, 0.02)
+    else:  # sgemm_test.cu:253-270: splitmix U(-1, 1), seeds +1..+4
+        a = orc.splitmix_uniform(M * K, seed + 1)
+        b = orc.splitmix_uniform(K * N, seed + 2)
+        c0 = orc.splitmix_uniform(M * N, seed + 3)
+        bias = orc.splitmix_uniform(N, seed + 4)
+    return (a.reshape((K, M) if ta else (M, K)), b.reshape((N, K) if tb else (K, N)),
+            c0.reshape(M, N), bias)
+
+
+def _sg_call(hk, fn, layout, A, B, C, M, N, K, alpha, beta, bias=None, bias_stride=0,
+             split_k=1, batch=1, sA=0, sB=0, sC=0):
+    lib = hk.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    lda, ldb = A.shape[-1], B.shape[-1]
+    bptr = 0 if bias is None else bias.data_ptr()
+    if fn == "hk_sgemm":
+        st = lib.hk_sgemm(layout, M, N, K, alpha, A.data_ptr(), lda, sA, B.data_ptr(), ldb, sB,
+                          beta, C.data_ptr(), N, sC, bptr, bias_stride, batch, split_k, stream)
+    elif fn == "hk_sgemm_addmm":
+        st = lib.hk_sgemm_addmm(M, N, K, alpha, A.data_ptr(), lda, sA, B.data_ptr(), ldb, sB,
+                                beta, bptr, bias_stride, C.data_ptr(), N, sC, batch, stream)
+    else:
+        st = lib.hk_sgemm_layout(layout, M, N, K, alpha, A.data_ptr(), lda, sA, B.data_ptr(),
+                                 ldb, sB, beta, C.data_ptr(), N, sC, batch, split_k, stream)
+    assert st == 0
+    torch.cuda.synchronize()
+    return C.cpu().numpy()
+
+
+@pytest.mark.parametrize("M,N,K", SG_HARNESS)
+@pytest.mark.parametrize("lay", ["NN", "NT", "TN"])
+@pytest.mark.parametrize("split_k", [1, 4])
+def test_sgemm_harness_sizes_bias_split_k(hk, orc, M, N, K, lay, split_k):
+    enum, ta, tb = SG_LAYOUT[lay]
+    say("sgemm", lay, M, N, K, split_k)
+    A, B, C0, bias = _sg_operands(orc, M, N, K, ta, tb, 7 + M)
+    out = _sg_call(hk, "hk_sgemm", enum, torch.from_numpy(A).to(DEV), torch.from_numpy(B).to(DEV),
+                   torch.from_numpy(C0).to(DEV), M, N, K, 1.5, 0.5,
+                   bias=torch.from_numpy(bias).to(DEV), bias_stride=N, split_k=split_k)
+    ref = orc.sgemm(ta, tb, A, B, alpha=1.5, beta=0.5, C0=C0, bias=bias)
+    assert max_rel(out, ref) <= 2e-3
+
+
+def test_sgemm_bias_strides_and_batches(hk, orc):
+    M, N, K, batch = 64, 96, 40, 3
+    say("sgemm bias strides")
+    As = [_sg_operands(orc, M, N, K, 0, 0, 50 + b) for b in range(batch)]
+    A = torch.from_numpy(np.stack([x[0] for x in As])).to(DEV)
+    B = torch.from_numpy(np.stack([x[1] for x in As])).to(DEV)
+    C0 = np.stack([x[2] for x in As])
+    full_bias = orc.splitmix_uniform(M * N, 77).reshape(M, N)
+    for stride, bias_np in ((N, As[0][3]), (M * N, full_bias.reshape(-1)), (1, full_bias[0, :1])):
+        for split_k in (1, 3):
+            C = torch.from_numpy(C0.copy()).to(DEV)
+            out = _sg_call(hk, "hk_sgemm", 2, A, B, C, M, N, K, 1.0, -0.5,
+                           bias=torch.from_numpy(np.ascontiguousarray(bias_np)).to(DEV),
+                           bias_stride=stride, split_k=split_k, batch=batch, sA=M * K, sB=K * N,
+                           sC=M * N)
+            for b in range(batch):
+                ref = orc.sgemm(0, 0, As[b][0], As[b][1], alpha=1.0, beta=-0.5, C0=C0[b])
+                if stride == N:
+                    ref = ref + bias_np
+                elif stride == M * N:  # the reference's (batch % M) * N row (core_template:310)
+                    ref = ref + full_bias[b % M]
+                else:
+                    ref = ref + bias_np[0]
+                assert max_rel(out[b], ref) <= 2e-3, (stride, split_k, b)
+
+
+def test_sgemm_addmm_beta_scaled_bias(hk, orc):
+    M, N, K = 256, 256, 256
+    say("sgemm addmm")
+    A, B, C0, bias = _sg_operands(orc, M, N, K, 0, 0, 90)
+    out = _sg_call(hk, "hk_sgemm_addmm", 2, torch.from_numpy(A).to(DEV),
+                   torch.from_numpy(B).to(DEV), torch.from_numpy(C0).to(DEV), M, N, K, 1.0, 0.5,
+                   bias=torch.from_numpy(bias).to(DEV), bias_stride=N)
+    ref = orc.sgemm(0, 0, A, B, alpha=1.0, beta=0.5, C0=C0) + 0.5 * bias
+    assert max_rel(out, ref) <= 2e-3
+
+
+@pytest.mark.parametrize("lay", ["NN", "NT", "TN"])
+def test_sgemm_tile_kernel_entry_point(hk, orc, lay):
+    enum, ta, tb = SG_LAYOUT[lay]
+    M, N, K = 512, 384, 128
+    say("sgemm layout entry", lay)
+    A, B, C0, _ = _sg_operands(orc, M, N, K, ta, tb, 120)
+    out = _sg_call(hk, "hk_sgemm_layout", enum, torch.from_numpy(A).to(DEV),
+                   torch.from_numpy(B).to(DEV), torch.from_numpy(C0).to(DEV), M, N, K, 1.0, 0.5,
+                   split_k=2)
+    assert max_rel(out, orc.sgemm(ta, tb, A, B, alpha=1.0, beta=0.5, C0=C0)) <= 2e-3
+
+
+@pytest.mark.parametrize("M,N,K,lay", [(17, 9, 33, "NN"), (33, 65, 7, "TN"), (5, 300, 41, "NT")])
+def test_sgemm_ragged(hk, orc, M, N, K, lay):
+    enum, ta, tb = SG_LAYOUT[lay]
+    say("sgemm ragged", M, N, K, lay)
+    A, B, C0, bias = _sg_operands(orc, M, N, K, ta, tb, 130)
+    out = _sg_call(hk, "hk_sgemm", enum, torch.from_numpy(A).to(DEV), torch.from_numpy(B).to(DEV),
+                   torch.from_numpy(C0).to(DEV), M, N, K, 1.0, 1.0,
+                   bias=torch.from_numpy(bias).to(DEV), bias_stride=N)
+    assert max_rel(out, orc.sgemm(ta, tb, A, B, alpha=1.0, beta=1.0, C0=C0, bias=bias)) <= 2e-3
+
+
+@pytest.mark.parametrize("lay", ["NN", "NT", "TN"])
+def test_sgemm_baseline_shape_split_k4_sampled_rows(hk, orc, lay):
+    # 4096^3, split-K 4, fused bias; 64 rows checked against the oracle.
+    enum, ta, tb = SG_LAYOUT[lay]
+    M = N = K = 4096
+    say("sgemm baseline", lay)
+    A, B, C0, bias = _sg_operands(orc, M, N, K, ta, tb, 140, normal=True)
+    out = _sg_call(hk, "hk_sgemm", enum, torch.from_numpy(A).to(DEV), torch.from_numpy(B).to(DEV),
+                   torch.from_numpy(C0).to(DEV), M, N, K, 1.0, 1.0,
+                   bias=torch.from_numpy(bias).to(DEV), bias_stride=N, split_k=4)
+    rows = np.unique(np.concatenate([np.arange(0, M, 67), [M - 1]]))
+    Asub = np.ascontiguousarray(A[:, rows] if ta else A[rows, :])
+    ref = orc.sgemm(ta, tb, Asub, B, alpha=1.0, beta=1.0, C0=np.ascontiguousarray(C0[rows]),
+                    bias=bias)
+    rel = max_rel(out[rows], ref)
+    print(f"sgemm baseline rel {rel:.2e}")
+    assert rel <= 2e-3
