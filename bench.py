@@ -217,6 +217,7 @@ def per_kernel_suite(flush):
     cases.append(("reduce_inner_16384x50304", lambda: hk.unified_reduce_sum(rs, lay, rdst),
                   16384 * 50304 * 4, "hbm"))
     cases += gemm_cases(g)
+    cases += attention_cases(g)
     for name, fn, work, bound in cases:
         t = time_kernel(fn, ARGS.reps, flush)
         if bound == "hbm":
@@ -230,6 +231,27 @@ def per_kernel_suite(flush):
                          "unit": "TFLOP/s", "peak": peak, "frac": round(ach / peak, 4)}
         log(name, out[name])
     return out
+
+
+def attention_cases(g):
+    """attention fwd and bwd, B=8 H=12 T=1024 d=64, fp32 I/O."""
+    A = W.ATTN
+    B, H, T, D = A["B"], A["H"], A["T"], A["d"]
+    q, k, v, do = (torch.randn(B, H, T, D, generator=g, device=DEV) for _ in range(4))
+    cases = []
+    for causal in (True, False):
+        o, lse = hk.fused_attn_forward(q, k, v, causal)
+        Dt = hk.attn_bwd_precompute_D(do, o)
+        dq, dk, dv = torch.zeros_like(q), torch.empty_like(k), torch.empty_like(v)
+        tag = "causal" if causal else "noncausal"
+        cases.append((f"attn_fwd_{tag}_8x12x1024x64",
+                      lambda c=causal, o=o, lse=lse: hk.fused_attn_forward(q, k, v, c, o=o, lse=lse),
+                      W.attn_fwd_flop(B, H, T, D, causal), "fp32_matrix"))
+        cases.append((f"attn_bwd_{tag}_8x12x1024x64",
+                      lambda c=causal, lse=lse, Dt=Dt, dq=dq, dk=dk, dv=dv: hk.attn_backward(
+                          q, k, v, do, lse, Dt, c, dq=dq, dk=dk, dv=dv),
+                      W.attn_bwd_flop(B, H, T, D, causal), "fp32_matrix"))
+    return cases
 
 
 def gemm_cases(g):

@@ -1,0 +1,288 @@
+// attention_fwd.hip - fused attention forward, fp32 I/O, head_dim 64, causal or not, with the
+// saved log-sum-exp; plus the backward pre-pass D = rowsum(dO * O).
+//
+// Reference behaviour:
+//   fused_attn_forward_kernel_tc_sm89<64, 64, 64, 1>
+//       kernels/attention/fused_attn_forward_kernel_tc_sm89.cu:72-426 (params :8-29):
+//       O = softmax(scale * Q K^T, key j <= query i when causal) V, LSE = max + ln(sum).
+//   mem_efficient_bwd_precompute_D_sm89<64>
+//       kernels/attention/mem_efficient_bwd_precompute_D_sm89.cu:45-91: D = rowsum(dO * O).
+//
+// Design (gfx950): one workgroup = 4 waves = 128 query rows of one (batch, head); a wave owns 32
+// queries. Products run on the fp32 MFMA v_mfma_f32_32x32x2_f32 (exact fp32 products; the
+// reference rounds operands to TF32). The score tile is formed transposed, S^T = K Q^T, so
+// each lane owns one query column: the online-softmax max is one 32-value register reduction
+// plus a single cross-half shuffle, the rescale factor is per lane, and the exponentiated
+// scores are already laid out as the B operand of the next product, O^T += V^T P^T, which
+// keeps O^T per lane as well (no LDS round trip of P, no cross-lane gathers of the rescale).
+// Q stays in registers (pre-scaled by scale * log2 e, so the softmax uses exp2); K and V tiles
+// of 64 keys go through two LDS stages (rows padded to 68 floats: conflict-free fragment
+// reads) with the next tile's global loads in flight. Causal workgroups are launched heaviest
+// first and stop at the diagonal.
+#include <mutex>
+
+#include "hk_device.h"
+#include "hk_host.h"
+
+static_assert(offsetof(hk_attn_fwd_params, T) == 48, "hk_attn_fwd_params layout");
+static_assert(offsetof(hk_attn_fwd_params, dropout_mask) == 72, "hk_attn_fwd_params layout");
+static_assert(sizeof(hk_attn_fwd_params) == 192, "hk_attn_fwd_params layout");
+static_assert(offsetof(hk_attn_bwd_params, B) == 80, "hk_attn_bwd_params layout");
+static_assert(offsetof(hk_attn_bwd_params, q_strideB) == 104, "hk_attn_bwd_params layout");
+static_assert(sizeof(hk_attn_bwd_params) == 328, "hk_attn_bwd_params layout");
+
+namespace {
+
+constexpr int kHD = 64;
+constexpr int kBQ = 128;                 // queries per workgroup (4 waves x 32)
+constexpr int kBKV = 64;                 // keys per K/V tile
+constexpr int kPitch = kHD + 4;          // LDS row pitch in floats
+constexpr int kTileFloats = kBKV * kPitch;
+constexpr size_t kLdsBytes = 2 * 2 * kTileFloats * sizeof(float);  // K and V, two stages
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// K/V tile loader: 64 rows x 64 floats = 1024 16-byte vectors per tensor; thread t moves vectors
+// t + 256 j (j = 0..3): 16 lanes cover one 256-byte row.
+struct KVLoader {
+  const float* k;
+  const float* v;
+  int64_t ks, vs;  // row strides (elements)
+  int64_t T;
+
+  __device__ void load(int64_t k0, float4 (&rk)[4], float4 (&rv)[4]) const {
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int f = threadIdx.x + 256 * j;
+      const int64_t row = k0 + (f >> 4);
+      const int col = (f & 15) * 4;
+      rk[j] = row < T ? *reinterpret_cast<const float4*>(k + row * ks + col) : zero;
+      rv[j] = row < T ? *reinterpret_cast<const float4*>(v + row * vs + col) : zero;
+    }
+  }
+  __device__ static void store(float* sk, float* sv, const float4 (&rk)[4], const float4 (&rv)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int f = threadIdx.x + 256 * j;
+      const int off = (f >> 4) * kPitch + (f & 15) * 4;
+      *reinterpret_cast<float4*>(sk + off) = rk[j];
+      *reinterpret_cast<float4*>(sv + off) = rv[j];
+    }
+  }
+};
+
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(hk_attn_fwd_params p) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  float* sK = lds;                       // [2][kTileFloats]
+  float* sV = lds + 2 * kTileFloats;     // [2][kTileFloats]
+
+  const int64_t T = p.T;
+  const int nqt = static_cast<int>((T + kBQ - 1) / kBQ);
+  const int qt = p.is_causal ? (nqt - 1 - static_cast<int>(blockIdx.x)) : static_cast<int>(blockIdx.x);
+  const int bh = blockIdx.y;
+  const int b = bh / p.nh, h = bh - b * p.nh;
+  const float* Qb = p.Q + b * p.q_strideB + h * p.q_strideH;
+  float* Ob = p.O + b * p.o_strideB + h * p.o_strideH;
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 31;
+  const int hh = lane >> 5;
+  const int64_t q0w = static_cast<int64_t>(qt) * kBQ + wave * 32;
+  const int64_t q = q0w + c;
+
+  // Q row (this lane's half of the head dim), scaled so that scores are in log2 units.
+  float qr[32];
+  {
+    const float qs = p.scale * kLog2e;
+    const float* qp = Qb + q * p.q_strideM + 32 * hh;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4 v = q < T ? *reinterpret_cast<const float4*>(qp + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+      qr[4 * j + 0] = v.x * qs;
+      qr[4 * j + 1] = v.y * qs;
+      qr[4 * j + 2] = v.z * qs;
+      qr[4 * j + 3] = v.w * qs;
+    }
+  }
+
+  f32x16_t o[2] = {f32x16_t{}, f32x16_t{}};  // O^T: d = 32 db + 8 (i/4) + 4 hh + i%4
+  float m = -INFINITY, l = 0.f;
+
+  const int64_t kv_end = p.is_causal ? (static_cast<int64_t>(qt) * kBQ + kBQ < T ? static_cast<int64_t>(qt) * kBQ + kBQ : T) : T;
+  const int nkv = static_cast<int>((kv_end + kBKV - 1) / kBKV);
+  KVLoader ld{p.K + b * p.k_strideB + h * p.k_strideH, p.V + b * p.v_strideB + h * p.v_strideH,
+              p.k_strideM, p.v_strideM, T};
+  float4 rk[4], rv[4];
+  if (nkv > 0) {
+    ld.load(0, rk, rv);
+    KVLoader::store(sK, sV, rk, rv);
+  }
+  __syncthreads();
+
+  for (int kt = 0; kt < nkv; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nkv;
+    if (more) ld.load(static_cast<int64_t>(kt + 1) * kBKV, rk, rv);
+    const int64_t k0 = static_cast<int64_t>(kt) * kBKV;
+    const float* k_st = sK + cur * kTileFloats;
+    const float* v_st = sV + cur * kTileFloats;
+    // a wave whose queries all precede this tile has nothing to add (causal)
+    if (!p.is_causal || k0 <= q0w + 31) {
+      f32x16_t s[2] = {f32x16_t{}, f32x16_t{}};
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const float* krow = k_st + (32 * kb + c) * kPitch + 32 * hh;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float4 kf = *reinterpret_cast<const float4*>(krow + 4 * j);
+          s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, qr[4 * j + 0], s[kb], 0, 0, 0);
+          s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qr[4 * j + 1], s[kb], 0, 0, 0);
+          s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qr[4 * j + 2], s[kb], 0, 0, 0);
+          s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qr[4 * j + 3], s[kb], 0, 0, 0);
+        }
+      }
+      // mask (causal: key > query; any: key >= T), tile max over this query's 64 keys
+      float mt = -INFINITY;
+      const bool need_mask = (p.is_causal && k0 + kBKV - 1 > q0w) || k0 + kBKV > T;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (need_mask) {
+            const int64_t key = k0 + 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
+            if (key >= T || (p.is_causal && key > q)) s[kb][i] = -INFINITY;
+          }
+          mt = fmaxf(mt, s[kb][i]);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 32, HK_WAVE));
+      const float m_new = fmaxf(m, mt);
+      // rows with nothing unmasked so far keep m = -inf and contribute nothing
+      const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m - m_new);
+      const float mref = (m_new == -INFINITY) ? 0.f : m_new;
+      float ls = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float e = exp2f(s[kb][i] - mref);
+          s[kb][i] = e;
+          ls += e;
+        }
+      l = l * alpha + ls;
+      m = m_new;
+#pragma unroll
+      for (int db = 0; db < 2; ++db) o[db] *= alpha;
+      // O^T[d][q] += sum_key V[key][d] P^T[key][q]
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
+            const float vv = v_st[key * kPitch + 32 * db + c];
+            o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, s[kb][i], o[db], 0, 0, 0);
+          }
+    }
+    if (more) KVLoader::store(sK + (cur ^ 1) * kTileFloats, sV + (cur ^ 1) * kTileFloats, rk, rv);
+    __syncthreads();
+  }
+
+  const float lt = l + __shfl_xor(l, 32, HK_WAVE);
+  if (q < T) {
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    float* orow = Ob + q * p.o_strideM;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * db + 8 * g + 4 * hh;
+        *reinterpret_cast<float4*>(orow + d) =
+            make_float4(o[db][4 * g + 0] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
+                        o[db][4 * g + 3] * inv);
+      }
+    if (hh == 0) {
+      float* lse = p.LSE + b * p.lse_strideB + h * p.lse_strideH;
+      lse[q] = (m + log2f(lt)) * kLn2;
+    }
+  }
+}
+
+// D[row] = sum_d dO[row][d] * O[row][d]: a wave per 4 rows, 16 lanes per 64-float row.
+__global__ __launch_bounds__(256) void attn_precompute_d_kernel(hk_attn_bwd_params p, int hd) {
+  const int bh = blockIdx.y;
+  const int b = bh / p.nh, h = bh - b * p.nh;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  float s = 0.f;
+  if (row < p.T) {
+    const float* o = p.O + b * p.o_strideB + h * p.o_strideH + row * p.o_strideM;
+    const float* d = p.dO + b * p.do_strideB + h * p.do_strideH + row * p.do_strideM;
+    for (int k = sub * 4; k < hd; k += 64) {
+      const float4 a = *reinterpret_cast<const float4*>(o + k);
+      const float4 g = *reinterpret_cast<const float4*>(d + k);
+      s += (a.x * g.x + a.y * g.y) + (a.z * g.z + a.w * g.w);
+    }
+  }
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 16);
+  if (row < p.T && sub == 0) p.D[b * p.d_strideB + h * p.d_strideH + row] = s;
+}
+
+bool rows_aligned(const void* base, int64_t strideB, int64_t strideH, int64_t strideM) {
+  return hk::aligned16(base) && strideB % 4 == 0 && strideH % 4 == 0 && strideM % 4 == 0;
+}
+
+}  // namespace
+
+extern "C" hipError_t hk_fused_attn_forward(const hk_attn_fwd_params* params, int head_dim,
+                                            hipStream_t stream) {
+  HK_CHECK_ARG(params != nullptr);
+  const hk_attn_fwd_params& p = *params;
+  HK_CHECK_ARG(head_dim == kHD);
+  HK_CHECK_ARG(p.B >= 0 && p.nh >= 0 && p.T >= 0);
+  if (p.B == 0 || p.nh == 0 || p.T == 0) return hipSuccess;
+  HK_CHECK_ARG(p.dropout_p == 0.0f);  // the dropout path is not provided by this build
+  HK_CHECK_ARG(p.Q && p.K && p.V && p.O && p.LSE);
+  HK_CHECK_ARG(rows_aligned(p.Q, p.q_strideB, p.q_strideH, p.q_strideM) &&
+               rows_aligned(p.K, p.k_strideB, p.k_strideH, p.k_strideM) &&
+               rows_aligned(p.V, p.v_strideB, p.v_strideH, p.v_strideM) &&
+               rows_aligned(p.O, p.o_strideB, p.o_strideH, p.o_strideM));
+  const int64_t bh = static_cast<int64_t>(p.B) * p.nh;
+  const int64_t nqt = (p.T + kBQ - 1) / kBQ;
+  HK_CHECK_ARG(bh <= 65535 && nqt <= INT32_MAX);
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [] {
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(kLdsBytes));
+  });
+  HK_RETURN_IF_ERROR(attr);
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3(static_cast<unsigned>(nqt), static_cast<unsigned>(bh)),
+                     dim3(256), kLdsBytes, stream, p);
+  return hk::launch_status();
+}
+
+extern "C" hipError_t hk_attn_bwd_precompute_D(const hk_attn_bwd_params* params, int head_dim,
+                                               hipStream_t stream) {
+  HK_CHECK_ARG(params != nullptr);
+  const hk_attn_bwd_params& p = *params;
+  // the reference instantiates HeadDim in {16, 32, 64, 128, 256} (precompute_D…:93-102)
+  HK_CHECK_ARG(head_dim > 0 && head_dim % 4 == 0 && head_dim <= 256);
+  HK_CHECK_ARG(p.B >= 0 && p.nh >= 0 && p.T >= 0);
+  if (p.B == 0 || p.nh == 0 || p.T == 0) return hipSuccess;
+  HK_CHECK_ARG(p.O && p.dO && p.D);
+  HK_CHECK_ARG(rows_aligned(p.O, p.o_strideB, p.o_strideH, p.o_strideM) &&
+               rows_aligned(p.dO, p.do_strideB, p.do_strideH, p.do_strideM));
+  const int64_t bh = static_cast<int64_t>(p.B) * p.nh;
+  HK_CHECK_ARG(bh <= 65535);
+  hipLaunchKernelGGL(attn_precompute_d_kernel,
+                     dim3(static_cast<unsigned>((p.T + 15) / 16), static_cast<unsigned>(bh)),
+                     dim3(256), 0, stream, p, head_dim);
+  return hk::launch_status();
+}

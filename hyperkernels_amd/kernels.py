@@ -240,6 +240,107 @@ class AdamPlan:
 
 
 # ----------------------------------------------------------------------------------------------
+# Attention (kernels/attention/*.cu), fp32, head_dim 64, tensors [B, nh, T, d] (any strides
+# with a unit last dimension), LSE / D [B, nh, T]
+# ----------------------------------------------------------------------------------------------
+_I64 = ctypes.c_int64
+
+
+class AttnFwdParams(ctypes.Structure):
+    """MemEfficientFwdParams (fused_attn_forward_kernel_tc_sm89.cu:8-29), field for field."""
+
+    _fields_ = [("Q", ctypes.c_void_p), ("K", ctypes.c_void_p), ("V", ctypes.c_void_p),
+                ("O", ctypes.c_void_p), ("LSE", ctypes.c_void_p), ("B", ctypes.c_int),
+                ("nh", ctypes.c_int), ("T", _I64), ("scale", ctypes.c_float),
+                ("is_causal", ctypes.c_bool), ("dropout_p", ctypes.c_float),
+                ("dropout_mask", ctypes.c_void_p)] + [
+        (f"{t}_stride{s}", _I64) for t in ("q", "k", "v", "o") for s in ("B", "M", "H")] + [
+        ("lse_strideB", _I64), ("lse_strideH", _I64)]
+
+
+class AttnBwdParams(ctypes.Structure):
+    """MemEfficientBwdParams (mem_efficient_bwd_precompute_D_sm89.cu:7-33), field for field."""
+
+    _fields_ = [(n, ctypes.c_void_p) for n in ("Q", "K", "V", "O", "dO", "LSE", "D", "dQ", "dK",
+                                               "dV")] + [
+        ("B", ctypes.c_int), ("nh", ctypes.c_int), ("T", ctypes.c_int), ("scale", ctypes.c_float),
+        ("is_causal", ctypes.c_bool)] + [
+        (f"{t}_stride{s}", _I64) for t in ("q", "k", "v", "o", "do", "dq", "dk", "dv")
+        for s in ("B", "M", "H")] + [
+        ("lse_strideB", _I64), ("lse_strideH", _I64), ("d_strideB", _I64), ("d_strideH", _I64)]
+
+
+def _set_strides(params, prefix: str, t: torch.Tensor) -> None:
+    if t.dim() != 4 or t.stride(-1) != 1:
+        raise ValueError("attention tensors are [B, nh, T, d] with a unit last-dim stride")
+    setattr(params, f"{prefix}_strideB", t.stride(0))
+    setattr(params, f"{prefix}_strideH", t.stride(1))
+    setattr(params, f"{prefix}_strideM", t.stride(2))
+
+
+def fused_attn_forward(q, k, v, causal: bool, scale: float | None = None, o=None, lse=None):
+    """fused_attn_forward_kernel_tc_sm89<64,64,64,1>: returns (O, LSE)."""
+    for t in (q, k, v):
+        if not t.is_cuda or t.dtype != torch.float32:
+            raise ValueError("fused_attn_forward: fp32 device tensors")
+    B, H, T, D = q.shape
+    scale = D ** -0.5 if scale is None else scale
+    o = torch.empty_like(q) if o is None else o
+    lse = torch.empty(B, H, T, device=q.device, dtype=torch.float32) if lse is None else lse
+    p = AttnFwdParams()
+    p.Q, p.K, p.V, p.O, p.LSE = (t.data_ptr() for t in (q, k, v, o, lse))
+    p.B, p.nh, p.T, p.scale, p.is_causal = B, H, T, scale, bool(causal)
+    p.dropout_p, p.dropout_mask = 0.0, None
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
+        _set_strides(p, name, t)
+    p.lse_strideB, p.lse_strideH = lse.stride(0), lse.stride(1)
+    call("hk_fused_attn_forward", ctypes.byref(p), D, _stream())
+    return o, lse
+
+
+def _bwd_params(q, k, v, o, do, lse, D, dq, dk, dv, causal, scale):
+    B, H, T, _ = q.shape
+    p = AttnBwdParams()
+    p.Q, p.K, p.V, p.O, p.dO, p.LSE, p.D, p.dQ, p.dK, p.dV = (
+        None if t is None else t.data_ptr() for t in (q, k, v, o, do, lse, D, dq, dk, dv))
+    p.B, p.nh, p.T, p.scale, p.is_causal = B, H, T, scale, bool(causal)
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", o), ("do", do), ("dq", dq), ("dk", dk),
+                    ("dv", dv)):
+        if t is not None:
+            _set_strides(p, name, t)
+    if lse is not None:
+        p.lse_strideB, p.lse_strideH = lse.stride(0), lse.stride(1)
+    p.d_strideB, p.d_strideH = D.stride(0), D.stride(1)
+    return p
+
+
+def attn_bwd_precompute_D(do, o, D=None):
+    """mem_efficient_bwd_precompute_D_sm89<HD>: D = rowsum(dO * O), [B, nh, T]."""
+    B, H, T, Dh = o.shape
+    D = torch.empty(B, H, T, device=o.device, dtype=torch.float32) if D is None else D
+    p = _bwd_params(o, None, None, o, do, None, D, None, None, None, False, 1.0)
+    p.Q = None
+    call("hk_attn_bwd_precompute_D", ctypes.byref(p), Dh, _stream())
+    return D
+
+
+def attn_backward(q, k, v, do, lse, D, causal: bool, scale: float | None = None, dq=None, dk=None,
+                  dv=None, o=None):
+    """OwnTensor::mem_efficient_bwd_unified_kernel_exp12<64, Causal>: returns (dQ, dK, dV).
+
+    dK and dV are written; dQ is ADDED into (zeroed here when not passed in), as in the
+    reference where the caller zeroes dQ before the launch."""
+    B, H, T, Dh = q.shape
+    scale = Dh ** -0.5 if scale is None else scale
+    dq = torch.zeros_like(q) if dq is None else dq
+    dk = torch.empty_like(k) if dk is None else dk
+    dv = torch.empty_like(v) if dv is None else dv
+    p = _bwd_params(q, k, v, o, do, lse, D, dq, dk, dv, causal, scale)
+    call("hk_attn_backward", ctypes.byref(p), Dh, _stream())
+    return dq, dk, dv
+
+
+# ----------------------------------------------------------------------------------------------
 # Unified reduce (kernels/reduction/unified_reduce_standalone.cu)
 # ----------------------------------------------------------------------------------------------
 REDUCE_INNER, REDUCE_OUTER, REDUCE_GENERIC = 0, 1, 2

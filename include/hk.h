@@ -19,6 +19,7 @@
 #ifndef HK_H_
 #define HK_H_
 
+#include <stdbool.h>
 #include <stddef.h>
 #include <stdint.h>
 #include <hip/hip_runtime_api.h>
@@ -262,6 +263,81 @@ HK_API hipError_t hk_sgemm_layout(int layout, int M, int N, int K, float alpha, 
                                   long long strideB, float beta, float* C, int ldc,
                                   long long strideC, int batchCount, int splitK,
                                   hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Attention, fp32 I/O, head_dim 64 (the reference's only instantiation), fp32 MFMA.
+ * Tensors are [B, nh, T, head_dim] with arbitrary batch/head/row strides (elements; last-dim
+ * stride 1; strides multiples of 4 and 16-byte aligned bases), LSE and D are [B, nh, T].
+ * The parameter blocks repeat the reference's field order and types exactly:
+ *   hk_attn_fwd_params = MemEfficientFwdParams
+ *     (kernels/attention/fused_attn_forward_kernel_tc_sm89.cu:8-29);
+ *   hk_attn_bwd_params = MemEfficientBwdParams
+ *     (kernels/attention/mem_efficient_bwd_precompute_D_sm89.cu:7-33; the OwnTensor copy,
+ *     mem_efficient_bwd_unified_kernel_exp12.cu:11-38, has the same layout).
+ * hk_fused_attn_forward replaces fused_attn_forward_kernel_tc_sm89<64, 64, 64, 1> (:72-74):
+ *   O = softmax(scale Q K^T [+ causal mask j <= i]) V, LSE = max + ln(sum of exp).
+ *   dropout_p must be 0 (the dropout path, :321-323, is not provided).
+ * hk_attn_bwd_precompute_D replaces mem_efficient_bwd_precompute_D_sm89<HeadDim> (:45-91):
+ *   D = rowsum(dO * O); head_dim any multiple of 4 up to 256.
+ * hk_attn_backward replaces OwnTensor::mem_efficient_bwd_unified_kernel_exp12<64, Causal>
+ *   (mem_efficient_bwd_unified_kernel_exp12.cu:54-56): from Q, K, V, dO, LSE and D it WRITES
+ *   dK and dV and ADDS into dQ (dQ accumulates atomically across key tiles, as in the
+ *   reference, so the caller zeroes dQ first; kernels_test.cu:562). is_causal selects the mask.
+ * ---------------------------------------------------------------------------------------- */
+typedef struct hk_attn_fwd_params {
+  const float* Q;
+  const float* K;
+  const float* V;
+  float* O;
+  float* LSE;
+  int B;
+  int nh;
+  int64_t T;
+  float scale;
+  bool is_causal;
+  float dropout_p;
+  const float* dropout_mask;
+  int64_t q_strideB, q_strideM, q_strideH;
+  int64_t k_strideB, k_strideM, k_strideH;
+  int64_t v_strideB, v_strideM, v_strideH;
+  int64_t o_strideB, o_strideM, o_strideH;
+  int64_t lse_strideB, lse_strideH;
+} hk_attn_fwd_params;
+
+typedef struct hk_attn_bwd_params {
+  const float* Q;
+  const float* K;
+  const float* V;
+  const float* O;
+  const float* dO;
+  const float* LSE;
+  float* D;
+  float* dQ;
+  float* dK;
+  float* dV;
+  int B;
+  int nh;
+  int T;
+  float scale;
+  bool is_causal;
+  int64_t q_strideB, q_strideM, q_strideH;
+  int64_t k_strideB, k_strideM, k_strideH;
+  int64_t v_strideB, v_strideM, v_strideH;
+  int64_t o_strideB, o_strideM, o_strideH;
+  int64_t do_strideB, do_strideM, do_strideH;
+  int64_t dq_strideB, dq_strideM, dq_strideH;
+  int64_t dk_strideB, dk_strideM, dk_strideH;
+  int64_t dv_strideB, dv_strideM, dv_strideH;
+  int64_t lse_strideB, lse_strideH;
+  int64_t d_strideB, d_strideH;
+} hk_attn_bwd_params;
+
+HK_API hipError_t hk_fused_attn_forward(const hk_attn_fwd_params* params, int head_dim,
+                                        hipStream_t stream);
+HK_API hipError_t hk_attn_bwd_precompute_D(const hk_attn_bwd_params* params, int head_dim,
+                                           hipStream_t stream);
+HK_API hipError_t hk_attn_backward(const hk_attn_bwd_params* params, int head_dim,
+                                   hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,183 @@
+"""GPU parity of fused attention (forward, precompute-D and backward) against the oracle's
+restatement of the harness's CPU FlashAttention reference (kernels_test.cu:68-139).
+Tolerance: BASELINE.json's max-rel 2e-3 (max|err| / max|ref|) for O, LSE, dQ, dK, dV."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import max_rel
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _qkv(orc, B, H, T, D, seeds, normal=False):
+    n = B * H * T * D
+    if normal:  # Q, K, V ~ N(0, 1)
+        return [orc.normal(n, s).reshape(B, H, T, D) for s in seeds]
+    return [orc.rand_uniform(n, s).reshape(B, H, T, D) for s in seeds]  # kernels_test.cu:499
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attn_forward_harness_shape(hk, orc, causal):
+    # kernels_test.cu:491-538: B=2, H=6, T=256, d=64, seeds 101..103, scale 1/sqrt(d)
+    B, H, T, D = 2, 6, 256, 64
+    say("attn fwd harness", causal)
+    q, k, v = _qkv(orc, B, H, T, D, (101, 102, 103))
+    scale = 1.0 / np.sqrt(np.float32(D))
+    o, lse = hk.fused_attn_forward(*(torch.from_numpy(a).to(DEV) for a in (q, k, v)), causal,
+                                   float(scale))
+    torch.cuda.synchronize()
+    ro, rl = orc.attn_forward(q, k, v, scale, causal)
+    assert max_rel(o.cpu().numpy(), ro) <= 2e-3
+    assert max_rel(lse.cpu().numpy(), rl) <= 2e-3
+    print(f"O rel {max_rel(o.cpu().numpy(), ro):.2e} LSE rel {max_rel(lse.cpu().numpy(), rl):.2e}")
+
+
+@pytest.mark.parametrize("T", [1, 33, 64, 100, 129, 300])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attn_forward_ragged_T(hk, orc, T, causal):
+    B, H, D = 1, 3, 64
+    say("attn fwd ragged", T, causal)
+    q, k, v = _qkv(orc, B, H, T, D, (11, 12, 13), normal=True)
+    o, lse = hk.fused_attn_forward(*(torch.from_numpy(a).to(DEV) for a in (q, k, v)), causal)
+    torch.cuda.synchronize()
+    ro, rl = orc.attn_forward(q, k, v, 0.125, causal)
+    assert max_rel(o.cpu().numpy(), ro) <= 2e-3
+    assert max_rel(lse.cpu().numpy(), rl) <= 2e-3
+
+
+def test_attn_forward_strided_bthd_layout(hk, orc):
+    # [B, T, H, d] storage viewed as [B, H, T, d] (non-contiguous head/row strides)
+    B, H, T, D = 2, 4, 192, 64
+    say("attn fwd strided")
+    q, k, v = _qkv(orc, B, H, T, D, (21, 22, 23), normal=True)
+    dev = [torch.from_numpy(np.ascontiguousarray(a.transpose(0, 2, 1, 3))).to(DEV).transpose(1, 2)
+           for a in (q, k, v)]
+    o = torch.empty(B, T, H, D, device=DEV).transpose(1, 2)
+    o, lse = hk.fused_attn_forward(*dev, True, o=o)
+    torch.cuda.synchronize()
+    ro, rl = orc.attn_forward(q, k, v, 0.125, True)
+    assert max_rel(o.cpu().numpy(), ro) <= 2e-3 and max_rel(lse.cpu().numpy(), rl) <= 2e-3
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attn_forward_baseline_shape_sampled_heads(hk, orc, causal):
+    # B=8, H=12, T=1024, d=64, Q, K, V ~ N(0, 1). The GPU computes all 96
+    # heads; the oracle checks 4 of them in full.
+    B, H, T, D = 8, 12, 1024, 64
+    say("attn fwd baseline", causal)
+    q, k, v = _qkv(orc, B, H, T, D, (31, 32, 33), normal=True)
+    o, lse = hk.fused_attn_forward(*(torch.from_numpy(a).to(DEV) for a in (q, k, v)), causal)
+    torch.cuda.synchronize()
+    o, lse = o.cpu().numpy(), lse.cpu().numpy()
+    for (b, h) in ((0, 0), (3, 7), (5, 2), (7, 11)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        ro, rl = orc.attn_forward(q[sl], k[sl], v[sl], 0.125, causal)
+        assert max_rel(o[sl], ro) <= 2e-3 and max_rel(lse[sl], rl) <= 2e-3, (b, h)
+    if causal:  # invariant: row 0 attends to key 0 only -> O[.,.,0] = V[.,.,0]
+        np.testing.assert_allclose(o[:, :, 0], v[:, :, 0], rtol=1e-5, atol=1e-6)
+
+
+def _bwd_check(hk, orc, q, k, v, do, causal, scale, from_gpu_forward=False):
+    ro, rl = orc.attn_forward(q, k, v, scale, causal)
+    rD, rdq, rdk, rdv = orc.attn_backward(q, k, v, ro, do, rl, scale, causal)
+    Q, K, V, dO = (torch.from_numpy(a).to(DEV) for a in (q, k, v, do))
+    if from_gpu_forward:  # the whole GPU chain: forward -> precompute D -> backward
+        O, L = hk.fused_attn_forward(Q, K, V, causal, scale)
+        Dt = hk.attn_bwd_precompute_D(dO, O)
+    else:  # the harness feeds the CPU reference's O, LSE and D (kernels_test.cu:559-561)
+        L, Dt = torch.from_numpy(rl).to(DEV), torch.from_numpy(rD).to(DEV)
+    dq, dk, dv = hk.attn_backward(Q, K, V, dO, L, Dt, causal, scale)
+    torch.cuda.synchronize()
+    # With a single key (T = 1) dS = P (dP - D) is an exact cancellation: the reference's dQ and
+    # dK are exactly zero and the GPU's are fp32 rounding residue; there the bound is taken
+    # relative to the size of the cancelling terms, |dO| |V|.
+    term = float(np.abs(do).max() * np.abs(v).max())
+    rels = [max_rel(g.cpu().numpy(), r) if np.abs(r).max() > 0
+            else float(np.abs(g.cpu().numpy()).max()) / term
+            for g, r in ((dq, rdq), (dk, rdk), (dv, rdv))]
+    print(f"dQ {rels[0]:.2e} dK {rels[1]:.2e} dV {rels[2]:.2e}")
+    assert max(rels) <= 2e-3, rels
+    return dq, rdq
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attn_backward_harness_shape(hk, orc, causal):
+    # kernels_test.cu:540-594: B=2, H=6, T=256, d=64, dO seed 104
+    B, H, T, D = 2, 6, 256, 64
+    say("attn bwd harness", causal)
+    q, k, v = _qkv(orc, B, H, T, D, (101, 102, 103))
+    do = orc.rand_uniform(B * H * T * D, 104).reshape(B, H, T, D)
+    _bwd_check(hk, orc, q, k, v, do, causal, float(1.0 / np.sqrt(np.float32(D))))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attn_backward_gpu_chain(hk, orc, causal):
+    B, H, T, D = 1, 4, 384, 64
+    say("attn bwd chain", causal)
+    q, k, v, do = _qkv(orc, B, H, T, D, (41, 42, 43, 44), normal=True)
+    _bwd_check(hk, orc, q, k, v, do, causal, 0.125, from_gpu_forward=True)
+
+
+@pytest.mark.parametrize("T", [1, 33, 100, 129, 300])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attn_backward_ragged_T(hk, orc, T, causal):
+    say("attn bwd ragged", T, causal)
+    q, k, v, do = _qkv(orc, 1, 2, T, 64, (51, 52, 53, 54), normal=True)
+    _bwd_check(hk, orc, q, k, v, do, causal, 0.125)
+
+
+def test_attn_backward_dq_accumulates(hk, orc):
+    # dQ is added into (the reference zeroes it before the launch and adds atomically)
+    say("attn bwd dq accumulate")
+    q, k, v, do = _qkv(orc, 1, 2, 128, 64, (61, 62, 63, 64), normal=True)
+    ro, rl = orc.attn_forward(q, k, v, 0.125, True)
+    rD = orc.attn_precompute_D(do, ro)
+    Q, K, V, dO = (torch.from_numpy(a).to(DEV) for a in (q, k, v, do))
+    L, Dt = torch.from_numpy(rl).to(DEV), torch.from_numpy(rD).to(DEV)
+    dq1, _, _ = hk.attn_backward(Q, K, V, dO, L, Dt, True, 0.125)
+    first = dq1.clone()
+    hk.attn_backward(Q, K, V, dO, L, Dt, True, 0.125, dq=dq1)
+    torch.cuda.synchronize()
+    assert max_rel(dq1.cpu().numpy(), 2 * first.cpu().numpy().astype(np.float64)) <= 1e-6
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attn_backward_baseline_shape_sampled_heads(hk, orc, causal):
+    # B=8, H=12, T=1024, d=64, dO ~ N(0, 1), forward's O / LSE reused.
+    # The GPU runs all 96 heads; the oracle checks 2 heads in full.
+    B, H, T, D = 8, 12, 1024, 64
+    say("attn bwd baseline", causal)
+    q, k, v, do = _qkv(orc, B, H, T, D, (71, 72, 73, 74), normal=True)
+    Q, K, V, dO = (torch.from_numpy(a).to(DEV) for a in (q, k, v, do))
+    O, L = hk.fused_attn_forward(Q, K, V, causal)
+    Dt = hk.attn_bwd_precompute_D(dO, O)
+    dq, dk, dv = hk.attn_backward(Q, K, V, dO, L, Dt, causal)
+    torch.cuda.synchronize()
+    dq, dk, dv = dq.cpu().numpy(), dk.cpu().numpy(), dv.cpu().numpy()
+    for (b, h) in ((0, 0), (6, 9)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        ro, rl = orc.attn_forward(q[sl], k[sl], v[sl], 0.125, causal)
+        _, rdq, rdk, rdv = orc.attn_backward(q[sl], k[sl], v[sl], ro, do[sl], rl, 0.125, causal)
+        rels = [max_rel(g[sl], r) for g, r in ((dq, rdq), (dk, rdk), (dv, rdv))]
+        print(f"head {(b, h)}: dQ {rels[0]:.2e} dK {rels[1]:.2e} dV {rels[2]:.2e}")
+        assert max(rels) <= 2e-3, rels
+
+
+def test_attn_precompute_D(hk, orc):
+    # kernels_test.cu:459-481 at the GPT shape: B=16, heads=12, T=1024, d=64, seeds 17/18
+    B, H, T, D = 16, 12, 1024, 64
+    say("precompute D")
+    do = orc.rand_uniform(B * H * T * D, 17).reshape(B, H, T, D)
+    o = orc.rand_uniform(B * H * T * D, 18).reshape(B, H, T, D)
+    Dt = hk.attn_bwd_precompute_D(torch.from_numpy(do).to(DEV), torch.from_numpy(o).to(DEV))
+    torch.cuda.synchronize()
+    ref = orc.attn_precompute_D(do, o)
+    assert max_rel(Dt.cpu().numpy(), ref) <= 1e-5
