@@ -217,10 +217,10 @@ def sparse_ce_forward(logits, targets):
     return loss, mx, sm
 
 
-def sparse_ce_backward(logits, targets, mx, sm, scale=1.0):
+def sparse_ce_backward(logits, targets, mx, sm, scale=1.0, out=None):
     logits = _c(logits)
     rows, vocab = logits.shape
-    grad = np.empty_like(logits)
+    grad = np.empty_like(logits) if out is None else out
     lib().oracle_sparse_ce_backward(logits, _c(targets, np.int32), _c(mx), _c(sm), grad, rows,
                                     vocab, scale)
     return grad
@@ -232,6 +232,14 @@ def adamw(p, g, m, v, lr, b1, b2, eps, wd, bc1, bc2):
     lib().oracle_adamw(p.reshape(-1), _c(g).reshape(-1), m.reshape(-1), v.reshape(-1), p.size, lr,
                        b1, b2, eps, wd, bc1, bc2)
     return p, m, v
+
+
+def adamw_(p, g, m, v, lr, b1, b2, eps, wd, bc1, bc2):
+    """In-place form of adamw on contiguous float32 arrays (no copies)."""
+    for a in (p, g, m, v):
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+    lib().oracle_adamw(p.reshape(-1), g.reshape(-1), m.reshape(-1), v.reshape(-1), p.size, lr,
+                       b1, b2, eps, wd, bc1, bc2)
 
 
 def reduce_inner(src, nout, length, row_stride=None):
