@@ -7,10 +7,10 @@
 //   backward  kernels/loss/sparseCENormalize_from_stats.cu:7-49
 //             grad_j = (exp(x_j - max) / sum - [j == target]) * (*grad_output * host_scale)
 //
-// Design (gfx950): one 256-lane workgroup streams one row. A row of fp32 logits starts at
+// Design (gfx950): one 1024-lane workgroup streams one row in the forward. A row of fp32 logits starts at
 // row * vocab * 4 bytes, which is only 4-byte aligned when vocab is odd (the GPT-2 vocabulary
 // 50257 is), so each row is split into a scalar head up to the next 16-byte boundary, a body
-// of 16-byte loads (each lane keeps 4 of them in flight), and a scalar tail. This is what lets
+// of 16-byte loads (each lane keeps 2 of them in flight), and a scalar tail. This is what lets
 // any vocab size work; the reference assumes vocab % 4 == 0. Each lane keeps an online
 // (max, sum) state, updated once per 4 values; lanes merge with 64-wide butterflies and the
 // four waves merge through LDS.
@@ -20,8 +20,6 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / HK_WAVE;
-constexpr int kUnroll = 4;
 
 __device__ __forceinline__ void absorb1(float& m, float& s, float v) {
   if (v > m) {
@@ -49,13 +47,20 @@ __device__ __forceinline__ void split_row(const void* p, int64_t n, int64_t& h, 
   nb = (n - h) >> 2;
 }
 
-__global__ __launch_bounds__(kThreads) void ce_forward(const float* __restrict__ logits,
-                                                       const int32_t* __restrict__ targets,
-                                                       float* __restrict__ losses,
-                                                       float* __restrict__ saved_max,
-                                                       float* __restrict__ saved_sum,
-                                                       int64_t vocab) {
-  __shared__ float red_m[kWaves], red_s[kWaves];
+// Forward workgroup: 1024 lanes per row with two 16-byte loads each in flight. A row is
+// ~200 KB, so a workgroup's life is a dozen dependent load rounds; wide workgroups shorten
+// that chain (measured on MI355X: 6.85 TB/s at 1024 lanes against 6.3 TB/s at 256).
+constexpr int kFwdThreads = 1024;
+constexpr int kFwdWaves = kFwdThreads / HK_WAVE;
+constexpr int kFwdUnroll = 2;
+
+__global__ __launch_bounds__(kFwdThreads) void ce_forward(const float* __restrict__ logits,
+                                                          const int32_t* __restrict__ targets,
+                                                          float* __restrict__ losses,
+                                                          float* __restrict__ saved_max,
+                                                          float* __restrict__ saved_sum,
+                                                          int64_t vocab) {
+  __shared__ float red_m[kFwdWaves], red_s[kFwdWaves];
   const int64_t row = blockIdx.x;
   const float* x = logits + row * vocab;
   const int tid = threadIdx.x;
@@ -66,15 +71,26 @@ __global__ __launch_bounds__(kThreads) void ce_forward(const float* __restrict__
   if (tid < h) absorb1(m, s, x[tid]);
   const float4* body = reinterpret_cast<const float4*>(x + h);
   int64_t i = tid;
-  for (; i + (kUnroll - 1) * kThreads < nb; i += kUnroll * kThreads) {
-    float4 v[kUnroll];
+  for (; i + (kFwdUnroll - 1) * kFwdThreads < nb; i += kFwdUnroll * kFwdThreads) {
+    float4 v[kFwdUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) v[u] = hk::ld_nt(body + i + u * kThreads);
+    for (int u = 0; u < kFwdUnroll; ++u) v[u] = hk::ld_nt(body + i + u * kFwdThreads);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) absorb4(m, s, v[u]);
+    for (int u = 0; u < kFwdUnroll; ++u) absorb4(m, s, v[u]);
   }
-  for (; i < nb; i += kThreads) absorb4(m, s, hk::ld_nt(body + i));
-  for (int64_t j = h + 4 * nb + tid; j < vocab; j += kThreads) absorb1(m, s, x[j]);
+  {  // remainder of the body: the same loads in flight, predicated
+    float4 v[kFwdUnroll];
+    bool ok[kFwdUnroll];
+#pragma unroll
+    for (int u = 0; u < kFwdUnroll; ++u) {
+      ok[u] = i + u * kFwdThreads < nb;
+      if (ok[u]) v[u] = hk::ld_nt(body + i + u * kFwdThreads);
+    }
+#pragma unroll
+    for (int u = 0; u < kFwdUnroll; ++u)
+      if (ok[u]) absorb4(m, s, v[u]);
+  }
+  for (int64_t j = h + 4 * nb + tid; j < vocab; j += kFwdThreads) absorb1(m, s, x[j]);
 
   hk::wave_softmax_merge(m, s);
   const int wave = tid >> 6;
@@ -86,7 +102,7 @@ __global__ __launch_bounds__(kThreads) void ce_forward(const float* __restrict__
   if (tid == 0) {
     float fm = red_m[0], fs = red_s[0];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) hk::softmax_merge(fm, fs, red_m[w], red_s[w]);
+    for (int w = 1; w < kFwdWaves; ++w) hk::softmax_merge(fm, fs, red_m[w], red_s[w]);
     saved_max[row] = fm;
     saved_sum[row] = fs;
     const int64_t t = static_cast<int64_t>(targets[row]);
@@ -101,13 +117,15 @@ __device__ __forceinline__ float ce_grad1(float v, float mx, float inv_sum, floa
 }
 
 // Vector path: logits and grad share the same 16-byte phase on every row. The row's body is cut
-// into chunks of kChunkVec 16-byte vectors, one workgroup each (grid = rows x chunks), and each
-// lane issues all of its kUnroll loads before computing: a short-lived workgroup with its
-// loads in flight keeps more bytes moving than one long loop per row. Chunk 0 also writes the
-// row's head, the last chunk its tail.
-constexpr int kChunkVec = kThreads * kUnroll;
+// into chunks of kBwdThreads 16-byte vectors, one workgroup each (grid = rows x chunks), one
+// vector per lane: many short-lived workgroups keep more bytes in flight across the device
+// than a few long ones (measured on MI355X at 8192 x 50257: ~6.2 TB/s with 512-vector
+// chunks against ~5.7 TB/s with 1024-vector chunks of four vectors per lane). Chunk 0 also
+// writes the row's head, the last chunk its tail.
+constexpr int kBwdThreads = 512;
+constexpr int kChunkVec = kBwdThreads;
 
-__global__ __launch_bounds__(kThreads) void ce_backward(
+__global__ __launch_bounds__(kBwdThreads) void ce_backward(
     const float* __restrict__ logits, const int32_t* __restrict__ targets,
     float* __restrict__ grad, const float* __restrict__ saved_max,
     const float* __restrict__ saved_sum, int64_t vocab, int nchunks,
@@ -117,42 +135,30 @@ __global__ __launch_bounds__(kThreads) void ce_backward(
   const float* x = logits + row * vocab;
   float* g = grad + row * vocab;
   const int tid = threadIdx.x;
+  int64_t h, nb;
+  split_row(x, vocab, h, nb);
+  const float4* xb = reinterpret_cast<const float4*>(x + h);
+  float4* gb = reinterpret_cast<float4*>(g + h);
+  const int64_t i = static_cast<int64_t>(chunk) * kChunkVec + tid;
+  float4 v;
+  if (i < nb) v = hk::ld_nt(xb + i);  // issued before the row statistics are needed
   const float mx = saved_max[row];
   const float inv_sum = 1.0f / saved_sum[row];
   const float scale = (grad_output ? grad_output[0] : 1.0f) * host_scale;
   const int64_t t = static_cast<int64_t>(targets[row]);
-
-  int64_t h, nb;
-  split_row(x, vocab, h, nb);
   if (chunk == 0 && tid < h) g[tid] = ce_grad1(x[tid], mx, inv_sum, scale, tid == t);
   if (chunk == nchunks - 1) {
     const int64_t j = h + 4 * nb + tid;
     if (j < vocab) g[j] = ce_grad1(x[j], mx, inv_sum, scale, j == t);
   }
-  const float4* xb = reinterpret_cast<const float4*>(x + h);
-  float4* gb = reinterpret_cast<float4*>(g + h);
-  // target position relative to this chunk's first element (32-bit: a chunk is 4096 values)
-  const int64_t base = static_cast<int64_t>(chunk) * kChunkVec;
-  const int64_t trel64 = t - h - 4 * base;
-  const int trel = (trel64 >= 0 && trel64 < 4 * kChunkVec) ? static_cast<int>(trel64) : -1;
-  float4 v[kUnroll];
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = base + tid + u * kThreads;
-    if (i < nb) v[u] = hk::ld_nt(xb + i);
-  }
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = base + tid + u * kThreads;
-    if (i < nb) {
-      const int j = 4 * (tid + u * kThreads);
-      float4 o;
-      o.x = ce_grad1(v[u].x, mx, inv_sum, scale, j + 0 == trel);
-      o.y = ce_grad1(v[u].y, mx, inv_sum, scale, j + 1 == trel);
-      o.z = ce_grad1(v[u].z, mx, inv_sum, scale, j + 2 == trel);
-      o.w = ce_grad1(v[u].w, mx, inv_sum, scale, j + 3 == trel);
-      hk::st_nt(gb + i, o);
-    }
+  if (i < nb) {
+    const int64_t j = h + 4 * i;
+    float4 o;
+    o.x = ce_grad1(v.x, mx, inv_sum, scale, j + 0 == t);
+    o.y = ce_grad1(v.y, mx, inv_sum, scale, j + 1 == t);
+    o.z = ce_grad1(v.z, mx, inv_sum, scale, j + 2 == t);
+    o.w = ce_grad1(v.w, mx, inv_sum, scale, j + 3 == t);
+    hk::st_nt(gb + i, o);
   }
 }
 
@@ -182,7 +188,7 @@ extern "C" hipError_t hk_sparse_ce_forward_f32_i32(const float* logits, const in
   HK_CHECK_ARG(batch_size >= 0 && vocab_size >= 1 && batch_size <= INT32_MAX);
   if (batch_size == 0) return hipSuccess;
   HK_CHECK_ARG(logits && targets && losses && saved_max && saved_sum);
-  hipLaunchKernelGGL(ce_forward, dim3(static_cast<unsigned>(batch_size)), dim3(kThreads), 0,
+  hipLaunchKernelGGL(ce_forward, dim3(static_cast<unsigned>(batch_size)), dim3(kFwdThreads), 0,
                      stream, logits, targets, losses, saved_max, saved_sum, vocab_size);
   return hk::launch_status();
 }
@@ -207,7 +213,7 @@ extern "C" hipError_t hk_sparse_ce_backward_f32_i32(const float* logits, const i
   const int64_t nchunks = hk::ceil_div(vocab_size / 4 + 1, kChunkVec);
   HK_CHECK_ARG(nchunks <= INT32_MAX && batch_size * nchunks <= INT32_MAX);
   hipLaunchKernelGGL(ce_backward, dim3(static_cast<unsigned>(batch_size * nchunks)),
-                     dim3(kThreads), 0, stream, logits, targets, grad, saved_max, saved_sum,
+                     dim3(kBwdThreads), 0, stream, logits, targets, grad, saved_max, saved_sum,
                      vocab_size, static_cast<int>(nchunks), grad_output, host_scale);
   return hk::launch_status();
 }

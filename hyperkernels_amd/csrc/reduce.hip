@@ -13,7 +13,7 @@
 // The split writes partials [split][num_outputs] to the library's per-device workspace and a
 // second kernel sums them in slice order, so results are deterministic and nothing is
 // allocated per call (the reference stages through freshly allocated memory and semaphores).
-//   inner:   a workgroup (256 lanes) per output row slice, 16-byte loads after a head peel
+//   inner:   a workgroup (512 lanes) per output row slice, 16-byte loads after a head peel
 //            when the row is long; a 64-lane wave per output when rows are short.
 //   outer:   a lane per output (consecutive lanes read consecutive columns), 8 rows in
 //            flight per lane, the reduced axis split over blockIdx.y.
@@ -30,18 +30,28 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / HK_WAVE;
 
 // ---- inner, long rows: workgroup per (output, slice) ----------------------------------------
-__global__ __launch_bounds__(kThreads) void reduce_inner_block(const float* __restrict__ src,
-                                                               float* __restrict__ dst,
-                                                               int64_t row_stride, int64_t len,
-                                                               int64_t slice_len, int64_t nout) {
-  __shared__ float red[kWaves];
+// 512 lanes with four 16-byte loads each in flight, the body's remainder included: a row
+// slice is a short chain of dependent load rounds, so lanes per row and loads per round set
+// the rate (measured on MI355X at 16384 x 50304: ~7.0 TB/s, against 5.6 TB/s for 256 lanes
+// with a one-load remainder loop).
+constexpr int kBlockThreads = 512;
+constexpr int kBlockWaves = kBlockThreads / HK_WAVE;
+constexpr int kBlockUnroll = 4;
+
+__global__ __launch_bounds__(kBlockThreads) void reduce_inner_block(const float* __restrict__ src,
+                                                                    float* __restrict__ dst,
+                                                                    int64_t row_stride,
+                                                                    int64_t len,
+                                                                    int64_t slice_len,
+                                                                    int64_t nout) {
+  __shared__ float red[kBlockWaves];
   const int64_t o = blockIdx.x;
   const int64_t s0 = static_cast<int64_t>(blockIdx.y) * slice_len;
   int64_t s1 = s0 + slice_len;
   if (s1 > len) s1 = len;
   const float* row = src + o * row_stride;
   const int tid = threadIdx.x;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float acc[kBlockUnroll] = {};
   if (s0 < s1) {
     const float* x = row + s0;
     const int64_t n = s1 - s0;
@@ -51,18 +61,26 @@ __global__ __launch_bounds__(kThreads) void reduce_inner_block(const float* __re
     if (tid < h) acc[0] += x[tid];
     const float4* b = reinterpret_cast<const float4*>(x + h);
     int64_t i = tid;
-    for (; i + 3 * kThreads < nb; i += 4 * kThreads) {
-      float4 v[4];
+    for (; i + (kBlockUnroll - 1) * kBlockThreads < nb; i += kBlockUnroll * kBlockThreads) {
+      float4 v[kBlockUnroll];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = hk::ld_nt(b + i + u * kThreads);
+      for (int u = 0; u < kBlockUnroll; ++u) v[u] = hk::ld_nt(b + i + u * kBlockThreads);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) acc[u] += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+      for (int u = 0; u < kBlockUnroll; ++u) acc[u] += (v[u].x + v[u].y) + (v[u].z + v[u].w);
     }
-    for (; i < nb; i += kThreads) {
-      const float4 v = b[i];
-      acc[1] += (v.x + v.y) + (v.z + v.w);
+    {  // remainder of the body, the same loads in flight, predicated
+      float4 v[kBlockUnroll];
+      bool ok[kBlockUnroll];
+#pragma unroll
+      for (int u = 0; u < kBlockUnroll; ++u) {
+        ok[u] = i + u * kBlockThreads < nb;
+        if (ok[u]) v[u] = hk::ld_nt(b + i + u * kBlockThreads);
+      }
+#pragma unroll
+      for (int u = 0; u < kBlockUnroll; ++u)
+        if (ok[u]) acc[u] += (v[u].x + v[u].y) + (v[u].z + v[u].w);
     }
-    for (int64_t j = h + 4 * nb + tid; j < n; j += kThreads) acc[2] += x[j];
+    for (int64_t j = h + 4 * nb + tid; j < n; j += kBlockThreads) acc[1] += x[j];
   }
   float v = hk::wave_sum((acc[0] + acc[1]) + (acc[2] + acc[3]));
   if ((tid & 63) == 0) red[tid >> 6] = v;
@@ -70,7 +88,7 @@ __global__ __launch_bounds__(kThreads) void reduce_inner_block(const float* __re
   if (tid == 0) {
     float t = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) t += red[w];
+    for (int w = 0; w < kBlockWaves; ++w) t += red[w];
     dst[static_cast<int64_t>(blockIdx.y) * nout + o] = t;
   }
 }
@@ -193,7 +211,7 @@ hipError_t reduce_inner(const float* src, float* dst, int64_t nout, int64_t len,
     out = static_cast<float*>(ws);
   }
   hipLaunchKernelGGL(reduce_inner_block, dim3(static_cast<unsigned>(nout), static_cast<unsigned>(split)),
-                     dim3(kThreads), 0, stream, src, out, row_stride, len, slice_len, nout);
+                     dim3(kBlockThreads), 0, stream, src, out, row_stride, len, slice_len, nout);
   HK_RETURN_IF_ERROR(hk::launch_status());
   if (split > 1) return finalize(out, dst, nout, static_cast<int>(split), stream);
   return hipSuccess;
