@@ -12,20 +12,24 @@
 // op(B) = B [K,N] (ldb >= N) or B^T with B stored [N,K] (ldb >= K).
 //
 // Design (gfx950, CDNA4):
-//   - Workgroup tile 256 x 256, k-step 64, 4 waves (2 x 2, one per SIMD); each wave owns a
+//   - Workgroup tile 256 x 256, k-tile 64, 4 waves (2 x 2, one per SIMD); each wave owns a
 //     128 x 128 block of C as 4 x 4 tiles of v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators
-//     per lane). Per 16-deep k step a wave issues 16 MFMAs against 8 LDS fragment reads.
-//   - Both operands live in LDS "k-contiguous" ([row][64 k] bf16, 128 B rows; chunk
-//     placement XOR-permuted so fragment reads and both store patterns are free of bank
-//     conflicts, see lds_off). An operand that is k-contiguous in HBM is copied as
-//     16-byte chunks; one that is M- or N-contiguous (A^T, plain B) is read as 8 x 8 bf16
-//     blocks along its contiguous axis and transposed in registers before the LDS store, so
-//     all four layouts share one compute loop and every HBM access is a 16-byte load.
-//   - Two LDS stages and two register stages: tile kt + 2 is being fetched from HBM/L2 while
-//     tile kt + 1 waits in registers and tile kt is multiplied; one barrier per k-tile.
-//   - Epilogue: accumulators are staged through LDS as fp32 (half a tile at a time) and written
-//     as 16-byte bf16 rows, with alpha and beta applied in fp32 and a single rounding (the
-//     reference rounds alpha*acc to bf16 and then blends beta*C in bf16 arithmetic).
+//     per lane). Per 16-deep k step a wave issues 16 MFMAs against 8 operand reads from LDS.
+//   - HBM/L2 -> LDS copies bypass registers (global_load_lds_dwordx4, 16 bytes per lane) into
+//     a 2-stage LDS ring: tile kt + 2 is copied while tile kt is multiplied, with one barrier
+//     per k-tile. K-major operands are stored [row][k] and read with ds_read_b128; M/N-major
+//     operands are stored as they lie in HBM, [k][row], and read with the gfx950 transposing
+//     LDS read (ds_read_b64_tr_b16), so no layout needs a register transpose. The bank
+//     placement of both is chosen through the per-lane source addresses of the copies.
+//   - Operand reads of the next k step are interleaved with the current step's MFMAs
+//     (sched_group_barrier), and the copies of the next tile with the last step's MFMAs.
+//   - Epilogue straight from registers: with the MFMA inputs swapped, each lane holds 4
+//     consecutive columns of one output row per accumulator quad; alpha / beta are applied in
+//     fp32 with one rounding to bf16 (v_cvt_pk_bf16_f32, round to nearest even) and 8 bytes
+//     are stored per quad (the reference rounds alpha * acc to bf16 and then blends beta * C
+//     in bf16 arithmetic).
+//   - Edges: rows past M (N) are read clamped to the last row and their outputs are not
+//     stored; k past the end of the (split's) range is zero-filled in LDS on the last k-tile.
 //   - Workgroup order: consecutive tiles go to one XCD (the hardware deals workgroups to the 8
 //     XCDs round-robin) in groups of 8 tile-rows, so each XCD's L2 sees a compact C region.
 //   - Split-K (the core-template entry point with splitK > 1): each split writes fp32 partials
@@ -41,105 +45,91 @@
 namespace {
 
 constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int kThreads = 256;                         // 4 waves, 2 x 2 over the tile
-constexpr int kWaveM = 128, kWaveN = 128;             // 4 x 4 MFMA tiles of 32 x 32 per wave
-constexpr int kTileElems = 256 * BK;                  // one operand stage, bf16 elements
-constexpr int kStagePitch = 128 + 4;                  // fp32 epilogue staging row pitch
-constexpr size_t kLdsMain = 2 * 2 * kTileElems * sizeof(uint16_t);                 // 131072
-constexpr size_t kLdsEpi = static_cast<size_t>(BM) * kStagePitch * sizeof(float);   // 135168
-constexpr size_t kLdsBytes = kLdsMain > kLdsEpi ? kLdsMain : kLdsEpi;
+constexpr int kStages = 2;                             // LDS ring depth (k-tiles)
+constexpr int kThreads = 256;                          // 4 waves, 2 x 2 over the tile
+constexpr int kWaveM = 128, kWaveN = 128;              // 4 x 4 MFMA tiles of 32 x 32 per wave
+constexpr int kStageBytes = 256 * BK * 2;              // one operand, one k-tile (32 KiB)
+constexpr int kLoadsPerWave = kStageBytes / 1024 / 4;  // 16-byte lane loads per operand per wave
+constexpr size_t kLdsBytes = static_cast<size_t>(kStages) * 2 * kStageBytes;  // 128 KiB
 
 typedef short bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+#define HK_LDS __attribute__((address_space(3)))
 
-// LDS layout of one operand stage: 256 rows x 64 k (bf16). A row is 128 bytes, i.e. one pass
-// over the 32 LDS banks; its eight 16-byte chunks are placed at chunk ^ f(row),
-// f(row) = (row ^ (row >> 3)) & 7. A 16-byte LDS access is served 8 lanes at a time, and with
-// this placement each group of 8 lanes touches 8 distinct chunk positions (all 32 banks) in the
-// three access patterns below:
-//   - MFMA fragment reads: 8 consecutive rows, one chunk (f = row ^ const);
-//   - k-major stores: one row, 8 chunks;
-//   - transposed stores: rows 8l + j for 8 consecutive l, one chunk (f = j ^ l).
-// Returns the offset in bf16 elements.
-__device__ __forceinline__ int lds_off(int row, int chunk) {
-  return row * 64 + ((chunk ^ ((row ^ (row >> 3)) & 7)) * 8);
+// 16-byte global -> LDS copy of one lane (global_load_lds_dwordx4): the wave's 64 lanes write
+// 1 KiB of LDS at m0 + 16 * lane. Written as inline asm on purpose: for the builtin, the
+// compiler assumes every later LDS read may alias the copy and waits for ALL of them to land
+// before any LDS read, which would serialise the load pipeline against the MFMA loop. Here the
+// kernel waits for the copies itself (vmcnt) before the barrier that publishes a stage.
+// Address = sbase (wave-uniform 64-bit, SGPRs) + voff (per-lane byte offset).
+__device__ __forceinline__ void copy16_to_lds(const void* sbase, int voff, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+               "s"(lds_addr));
 }
 
-// Transposes an 8 x 8 block of bf16: in[r] holds 8 values of row r (two per 32-bit word, lower
-// index in the low half); out[c] receives column c.
-__device__ __forceinline__ void transpose8x8(const uint4 (&in)[8], uint4 (&out)[8]) {
-  const uint32_t* w[8];
-#pragma unroll
-  for (int r = 0; r < 8; ++r) w[r] = reinterpret_cast<const uint32_t*>(&in[r]);
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    uint32_t o[4];
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint32_t a = w[2 * d][c >> 1], b = w[2 * d + 1][c >> 1];
-      o[d] = (c & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
-    }
-    out[c] = make_uint4(o[0], o[1], o[2], o[3]);
-  }
-}
-
-// One operand's share of a k-tile (256 rows of M or N x 64 k), 8 16-byte loads per thread.
-// KMAJOR (element (row, k) at base[row * ld + k]): thread tt loads chunk tt % 8 of rows
-//   tt / 8 + 32 j; eight lanes read one contiguous 128-byte row segment.
-// otherwise (element at base[k * ld + row]): thread tt owns the 8 x 8 block of rows
-//   8 (tt % 32) .. +8 and k chunk tt / 32, read as 8 k-rows of 16 bytes (32 lanes read 512
-//   contiguous bytes) and transposed in registers.
+// One operand of a k-tile in LDS: 256 rows of M (or N) by BK = 64 k, bf16, 32 KiB.
+//
+// K-major operands (element (row, k) at base[row * ld + k]) are stored [row][64 k]: 128-byte
+// rows whose eight 16-byte chunks sit at chunk ^ (row & 7). A wave's copy instruction moves
+// 8 rows (lane l: row l / 8, stored chunk l % 8, which is global chunk (l % 8) ^ (row & 7), so
+// each row's 128 contiguous bytes are read by 8 lanes). The MFMA operand of a lane is 8
+// consecutive k of one row, one ds_read_b128; 8 consecutive lanes read 8 consecutive rows at
+// 8 distinct chunk positions, i.e. all 32 banks once.
+//
+// M/N-major operands (element at base[k * ld + row]) are stored as in HBM, [64 k][256 rows]:
+// 512-byte k-rows whose 16-byte chunks sit at chunk ^ (2 * (krow & 3)). A copy instruction
+// moves 2 k-rows (32 lanes read one contiguous 512-byte row segment). The MFMA operand (8
+// consecutive k of one row/column) is gathered with two ds_read_b64_tr_b16: within each
+// 16-lane group, lane j reads 4 bf16 of k-row kb + j / 4 at columns c0 + 4 (j % 4) and the
+// hardware transposes the 16 x 4 block so lane i receives column c0 + i, k = kb .. kb + 3. The
+// 16 lanes of one read touch 4 k-rows x 32 bytes; the chunk permutation spreads them over all
+// 32 banks.
 template <bool KMAJOR>
-struct TileLoader {
-  const uint16_t* base;
-  int64_t ld;
-  int rows, K;
-  int rbase;  // first global row of this tile
-  int tt;
-
-  __device__ void init(const uint16_t* b, int64_t l, int nrows, int k, int tile_row0, int t) {
-    base = b;
-    ld = l;
-    rows = nrows;
-    K = k;
-    rbase = tile_row0;
-    tt = t;
-  }
-
-  __device__ void load(int k0, uint4 (&reg)[8]) const {
-    const uint4 zero = make_uint4(0, 0, 0, 0);
+struct TileOperand {
+  // Byte offset of lane `lane`'s 16 bytes of copy instruction ii (0 .. 31) from the tile's
+  // global base at k = 0, and the (row, k) of its first element.
+  __device__ static void source(int ii, int lane, int64_t ld, int& row, int& k) {
     if (KMAJOR) {
-      const int k = k0 + (tt & 7) * 8;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int r = rbase + (tt >> 3) + 32 * j;
-        reg[j] = (r < rows && k < K)
-                     ? *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(r) * ld + k)
-                     : zero;
-      }
+      row = ii * 8 + (lane >> 3);
+      k = ((lane & 7) ^ (row & 7)) * 8;
     } else {
-      const int r = rbase + (tt & 31) * 8;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int k = k0 + (tt >> 5) * 8 + j;
-        reg[j] = (r < rows && k < K)
-                     ? *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(k) * ld + r)
-                     : zero;
-      }
+      k = ii * 2 + (lane >> 5);
+      row = ((lane & 31) ^ (2 * (k & 3))) * 8;
     }
   }
-
-  __device__ void store(uint16_t* stage, const uint4 (&reg)[8]) const {
+  __device__ static int64_t byte_offset(int row, int k, int64_t ld) {
+    return KMAJOR ? 2 * (static_cast<int64_t>(row) * ld + k)
+                  : 2 * (static_cast<int64_t>(k) * ld + row);
+  }
+  // Global step of one k-tile (elements).
+  __device__ static int64_t ktile_step(int64_t ld) { return KMAJOR ? BK : BK * ld; }
+  // LDS byte offset of the MFMA operand of MFMA block b (32 rows at wave offset wo),
+  // 16-deep k step s; `half` selects the second 4-k read of an M/N-major operand.
+  __device__ static int frag(int wo, int b, int s, int half, int lane) {
     if (KMAJOR) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        *reinterpret_cast<uint4*>(stage + lds_off((tt >> 3) + 32 * j, tt & 7)) = reg[j];
+      const int row = wo + b * 32 + (lane & 31);
+      const int c = 2 * s + (lane >> 5);
+      return row * 128 + ((c ^ (row & 7)) * 16);
     } else {
-      uint4 t[8];
-      transpose8x8(reg, t);
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        *reinterpret_cast<uint4*>(stage + lds_off((tt & 31) * 8 + j, tt >> 5)) = t[j];
+      const int g = lane >> 4, j = lane & 15;
+      const int col = wo + b * 32 + 16 * (g & 1) + 4 * (j & 3);
+      const int krow = 16 * s + 8 * (g >> 1) + (j >> 2) + 4 * half;
+      return krow * 512 + (((col >> 3) ^ (2 * (krow & 3))) * 16) + (col & 7) * 2;
+    }
+  }
+  __device__ static bf16x8_t read(const unsigned char HK_LDS* st, int wo, int b, int s,
+                                  int lane) {
+    if (KMAJOR) {
+      return *reinterpret_cast<const bf16x8_t HK_LDS*>(st + frag(wo, b, s, 0, lane));
+    } else {
+      const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (bf16x4_t HK_LDS*)(st + frag(wo, b, s, 0, lane)));
+      const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (bf16x4_t HK_LDS*)(st + frag(wo, b, s, 1, lane)));
+      return bf16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
   }
 };
@@ -159,38 +149,38 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
   tn = in_group / gsz;
 }
 
-// 16 MFMAs per 16-deep k step against 8 fragment reads.
-__device__ __forceinline__ void mma_stage(const uint16_t* a_st, const uint16_t* b_st, int wm,
-                                          int wn, int lane, f32x16_t (&acc)[4][4]) {
-  const int frow = lane & 31;
-  const int fch = lane >> 5;
-#pragma unroll
-  for (int s = 0; s < BK / 16; ++s) {
-    bf16x8_t af[4], bfr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      af[i] = *reinterpret_cast<const bf16x8_t*>(a_st + lds_off(wm * kWaveM + i * 32 + frow,
-                                                                s * 2 + fch));
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      bfr[j] = *reinterpret_cast<const bf16x8_t*>(b_st + lds_off(wn * kWaveN + j * 32 + frow,
-                                                                 s * 2 + fch));
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+// Scheduling hint: NR LDS reads spread over NM MFMAs (reads first in each pair), so the
+// operands of the next k step are fetched while the current one multiplies.
+template <int NM, int NR, int Q = 0>
+__device__ __forceinline__ void interleave_reads() {
+  if constexpr (Q < NM) {
+    constexpr int per = (NR + NM - 1) / NM;
+    constexpr int left = NR - Q * per;
+    constexpr int n = left <= 0 ? 0 : (left < per ? left : per);
+    if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x100, n, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    interleave_reads<NM, NR, Q + 1>();
   }
 }
 
+// Main loop per k-tile kt (ring slot kt % 2), 4 k steps of 16 MFMAs each:
+//   steps 0-2: operands of step s+1 are read from LDS between the MFMAs of step s;
+//   step 3:    wait for this wave's copies of tile kt+1, barrier (tile kt+1 visible to all,
+//              every wave done reading slot kt % 2), read step 0 of tile kt+1, and issue the
+//              copies of tile kt+2 into slot kt % 2 between the 16 MFMAs.
+// The operands are swapped in the MFMA (B block as the "A" input), so each lane ends up
+// holding 4 consecutive output columns of one output row per register quad: the epilogue
+// writes 8 bytes per quad straight from registers.
 template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL>
 __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
     int M, int N, int K, float alpha, const uint16_t* __restrict__ A, int64_t lda, int64_t sA,
     const uint16_t* __restrict__ B, int64_t ldb, int64_t sB, float beta, uint16_t* __restrict__ C,
     int64_t ldc, int64_t sC, int split_k, int k_per_split, float* __restrict__ part) {
+  using OA = TileOperand<A_KMAJOR>;
+  using OB = TileOperand<B_KMAJOR>;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
-  uint16_t* sA_st = reinterpret_cast<uint16_t*>(lds_raw);           // [2][256*64]
-  uint16_t* sB_st = sA_st + 2 * kTileElems;                         // [2][256*64]
+  unsigned char HK_LDS* ldsA = (unsigned char HK_LDS*)lds_raw;
+  unsigned char HK_LDS* ldsB = ldsA + kStages * kStageBytes;
 
   const int batch = blockIdx.z / split_k;
   const int split = blockIdx.z - batch * split_k;
@@ -199,17 +189,61 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
   tile_coords(tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int kbeg = split * k_per_split;
-  const int kend = min(K, kbeg + k_per_split);
+  const int klen = min(K, kbeg + k_per_split) - kbeg;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  TileLoader<A_KMAJOR> la;
-  TileLoader<B_KMAJOR> lb;
-  la.init(A + static_cast<int64_t>(batch) * sA, lda, M, kend, m0, tid);
-  lb.init(B + static_cast<int64_t>(batch) * sB, ldb, N, kend, n0, tid);
+  // Tile bases at k = kbeg (wave-uniform) and per-lane source offsets of this wave's copy
+  // instructions. Rows past M (N) are clamped to the last row: they only feed outputs that
+  // are not stored. k past the split's end is zero-filled on the last k-tile (tail_fill).
+  const unsigned char* gA = reinterpret_cast<const unsigned char*>(
+      A + static_cast<int64_t>(batch) * sA +
+      (A_KMAJOR ? static_cast<int64_t>(m0) * lda + kbeg : static_cast<int64_t>(kbeg) * lda + m0));
+  const unsigned char* gB = reinterpret_cast<const unsigned char*>(
+      B + static_cast<int64_t>(batch) * sB +
+      (B_KMAJOR ? static_cast<int64_t>(n0) * ldb + kbeg : static_cast<int64_t>(kbeg) * ldb + n0));
+  int offA[kLoadsPerWave], offB[kLoadsPerWave];
+  int kA[kLoadsPerWave], kB[kLoadsPerWave];
+#pragma unroll
+  for (int i = 0; i < kLoadsPerWave; ++i) {
+    int row, k;
+    OA::source(wave * kLoadsPerWave + i, lane, lda, row, k);
+    row = min(row, (A_KMAJOR ? M - 8 + 7 : M - 8) - m0);  // k-major: a row; else an 8-row chunk
+    offA[i] = static_cast<int>(OA::byte_offset(row, k, lda));
+    kA[i] = k;
+    OB::source(wave * kLoadsPerWave + i, lane, ldb, row, k);
+    row = min(row, (B_KMAJOR ? N - 8 + 7 : N - 8) - n0);
+    offB[i] = static_cast<int>(OB::byte_offset(row, k, ldb));
+    kB[i] = k;
+  }
+  const int64_t stepA = 2 * OA::ktile_step(lda), stepB = 2 * OB::ktile_step(ldb);
+  const unsigned ldsA_addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(ldsA));
+  const unsigned ldsB_addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(ldsB));
+  const int ktiles = (klen + BK - 1) / BK;
+  const bool tail = (klen % BK) != 0;  // last k-tile is partial
+
+  // Copy q (0 .. 2 * kLoadsPerWave - 1) of k-tile kt into ring slot `slot`. On a partial last
+  // k-tile, lanes whose 8 k values lie past the split's end store zeros instead.
+  auto copy = [&](int kt, int slot, int q, bool fill) {
+    const bool isA = q < kLoadsPerWave;
+    const int i = isA ? q : q - kLoadsPerWave;
+    const unsigned char* base = (isA ? gA + kt * stepA : gB + kt * stepB);
+    const int off = isA ? offA[i] : offB[i];
+    const unsigned lds = (isA ? ldsA_addr : ldsB_addr) + slot * kStageBytes +
+                         (wave * kLoadsPerWave + i) * 1024;
+    if (!fill) {
+      copy16_to_lds(base, off, lds);
+    } else if (kt * BK + (isA ? kA[i] : kB[i]) < klen) {
+      copy16_to_lds(base, off, lds);
+    } else {
+      typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+      *reinterpret_cast<u32x4_t HK_LDS*>((unsigned char HK_LDS*)(uintptr_t)lds + 16 * lane) =
+          u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  constexpr int kCopies = 2 * kLoadsPerWave;
 
   f32x16_t acc[4][4];
 #pragma unroll
@@ -217,95 +251,125 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
 
-  // The next k-tile's global loads are in flight while the current one is multiplied.
-  uint4 ra[8], rb[8];
-  const int ktiles = (kend - kbeg + BK - 1) / BK;
+#pragma unroll
+  for (int p = 0; p < kStages; ++p)
+    if (p < ktiles) {
+      const bool fill = tail && p == ktiles - 1;
+#pragma unroll
+      for (int q = 0; q < kCopies; ++q) copy(p, p, q, fill);
+    }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+
+  bf16x8_t fa[2][4], fb[2][4];
   if (ktiles > 0) {
-    la.load(kbeg, ra);
-    lb.load(kbeg, rb);
-    la.store(sA_st, ra);
-    lb.store(sB_st, rb);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[0][i] = OA::read(ldsA, wm * kWaveM, i, 0, lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fb[0][j] = OB::read(ldsB, wn * kWaveN, j, 0, lane);
   }
-  __syncthreads();
+  constexpr int kReadsPerStep = (A_KMAJOR ? 4 : 8) + (B_KMAJOR ? 4 : 8);
+
   for (int kt = 0; kt < ktiles; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < ktiles;
-    if (more) {
-      la.load(kbeg + (kt + 1) * BK, ra);
-      lb.load(kbeg + (kt + 1) * BK, rb);
+    const int slot = kt & 1;
+    const unsigned char HK_LDS* sa = ldsA + slot * kStageBytes;
+    const unsigned char HK_LDS* sb = ldsB + slot * kStageBytes;
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s + 1 < BK / 16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fa[nxt][i] = OA::read(sa, wm * kWaveM, i, s + 1, lane);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fb[nxt][j] = OB::read(sb, wn * kWaveN, j, s + 1, lane);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[cur][j], fa[cur][i],
+                                                                acc[i][j], 0, 0, 0);
+        interleave_reads<16, kReadsPerStep>();
+      } else {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        if (kt + 1 < ktiles) {
+          const unsigned char HK_LDS* na = ldsA + (slot ^ 1) * kStageBytes;
+          const unsigned char HK_LDS* nb = ldsB + (slot ^ 1) * kStageBytes;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) fa[nxt][i] = OA::read(na, wm * kWaveM, i, 0, lane);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) fb[nxt][j] = OB::read(nb, wn * kWaveN, j, 0, lane);
+        }
+        const bool more = kt + kStages < ktiles;
+        const bool fill = tail && kt + kStages == ktiles - 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[cur][j], fa[cur][i],
+                                                                acc[i][j], 0, 0, 0);
+            const int q = i * 4 + j;
+            if (more && q < kCopies) copy(kt + kStages, slot, q, fill);
+          }
+        if (kCopies > 16 && more) {
+#pragma unroll
+          for (int q = 16; q < kCopies; ++q) copy(kt + kStages, slot, q, fill);
+        }
+      }
     }
-    mma_stage(sA_st + cur * kTileElems, sB_st + cur * kTileElems, wm, wn, lane, acc);
-    if (more) {
-      la.store(sA_st + (cur ^ 1) * kTileElems, ra);
-      lb.store(sB_st + (cur ^ 1) * kTileElems, rb);
-    }
-    __syncthreads();
   }
 
-  // Accumulator (i, j, r) of this lane sits at tile row wm*128 + i*32 + 8*(r/4) + 4*(lane/32)
-  // + r%4 and tile column wn*128 + j*32 + lane%32.
-  const int lrow = 4 * (lane >> 5);
-  const int lcol = lane & 31;
+  // Epilogue. Lane l holds, for MFMA block (i, j) and quad q, output row
+  // wm*128 + 32 i + l % 32 and columns wn*128 + 32 j + 8 q + 4 (l / 32) .. +3.
+  const int row0 = m0 + wm * kWaveM + (lane & 31);
+  const int col0 = n0 + wn * kWaveN + 4 * (lane >> 5);
   if (PARTIAL) {
     float* out = part + (static_cast<int64_t>(split) * (gridDim.z / split_k) + batch) *
                             static_cast<int64_t>(M) * N;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
+      const int row = row0 + 32 * i;
+      if (row >= M) continue;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * kWaveM + i * 32 + 8 * (r >> 2) + lrow + (r & 3);
-          const int col = n0 + wn * kWaveN + j * 32 + lcol;
-          if (row < M && col < N) out[static_cast<int64_t>(row) * N + col] = acc[i][j][r];
+        for (int q = 0; q < 4; ++q) {
+          const int col = col0 + 32 * j + 8 * q;
+          if (col < N)
+            *reinterpret_cast<float4*>(out + static_cast<int64_t>(row) * N + col) =
+                make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                            acc[i][j][4 * q + 3]);
         }
+    }
     return;
   }
-
-  float* stage = reinterpret_cast<float*>(lds_raw);
   uint16_t* Cb = C + static_cast<int64_t>(batch) * sC;
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    if (wn == half) {
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + 32 * i;
+    if (row >= M) continue;
+    uint16_t* crow = Cb + static_cast<int64_t>(row) * ldc;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int row = wm * kWaveM + i * 32 + 8 * (r >> 2) + lrow + (r & 3);
-            stage[row * kStagePitch + j * 32 + lcol] = acc[i][j][r];
-          }
-    }
-    __syncthreads();
-#pragma unroll 4
-    for (int it = 0; it < 16; ++it) {
-      const int q = tid + it * kThreads;
-      const int row = q >> 4;
-      const int c8 = (q & 15) * 8;
-      const int grow = m0 + row;
-      const int gcol = n0 + half * 128 + c8;
-      if (grow < M && gcol < N) {
-        const float4 v0 = *reinterpret_cast<const float4*>(stage + row * kStagePitch + c8);
-        const float4 v1 = *reinterpret_cast<const float4*>(stage + row * kStagePitch + c8 + 4);
-        float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        uint4* dst = reinterpret_cast<uint4*>(Cb + static_cast<int64_t>(grow) * ldc + gcol);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] *= alpha;
+      for (int q = 0; q < 4; ++q) {
+        const int col = col0 + 32 * j + 8 * q;
+        if (col >= N) continue;
+        f32x2_t lo = f32x2_t{acc[i][j][4 * q], acc[i][j][4 * q + 1]} * alpha;
+        f32x2_t hi = f32x2_t{acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]} * alpha;
+        uint2* dst = reinterpret_cast<uint2*>(crow + col);
         if (beta != 0.0f) {
-          const uint4 old = *dst;
-          const uint32_t ow[4] = {old.x, old.y, old.z, old.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            f[2 * e] += beta * __uint_as_float(ow[e] << 16);
-            f[2 * e + 1] += beta * __uint_as_float(ow[e] & 0xffff0000u);
-          }
+          const uint2 old = *dst;
+          lo += beta * f32x2_t{__uint_as_float(old.x << 16), __uint_as_float(old.x & 0xffff0000u)};
+          hi += beta * f32x2_t{__uint_as_float(old.y << 16), __uint_as_float(old.y & 0xffff0000u)};
         }
-        *dst = make_uint4(hk::pack_bf16x2(f[0], f[1]), hk::pack_bf16x2(f[2], f[3]),
-                          hk::pack_bf16x2(f[4], f[5]), hk::pack_bf16x2(f[6], f[7]));
+        const bf16x2_t blo = __builtin_convertvector(lo, bf16x2_t);
+        const bf16x2_t bhi = __builtin_convertvector(hi, bf16x2_t);
+        uint2 v;
+        __builtin_memcpy(&v.x, &blo, 4);
+        __builtin_memcpy(&v.y, &bhi, 4);
+        *dst = v;
       }
-    }
-    __syncthreads();
   }
 }
 
@@ -419,7 +483,9 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
   const bool tiled_ok = (contig_a % 8 == 0) && (contig_b % 8 == 0) && (N % 8 == 0) &&
                         (lda % 8 == 0) && (ldb % 8 == 0) && (ldc % 8 == 0) &&
                         (strideA % 8 == 0) && (strideB % 8 == 0) && (strideC % 8 == 0) &&
-                        hk::aligned16(A) && hk::aligned16(B) && hk::aligned16(C) && K > 0;
+                        hk::aligned16(A) && hk::aligned16(B) && hk::aligned16(C) && K > 0 &&
+                        // per-lane source offsets inside a tile are 32-bit byte offsets
+                        lda < (1 << 22) && ldb < (1 << 22);
   if (!tiled_ok) {
     if (K == 0) splitK = 1;
     dim3 grid((N + 15) / 16, (M + 15) / 16, batchCount);

@@ -107,7 +107,10 @@ def test_bgemm_backward_entry_points(hk, orc):
 
 
 @pytest.mark.parametrize("M,N,K,ta,tb", [(17, 9, 33, 0, 0), (33, 65, 7, 1, 1), (64, 64, 8, 1, 0),
-                                         (300, 260, 72, 0, 1)])
+                                         (300, 260, 72, 0, 1),
+                                         # MFMA path with partial M / N tiles and a K tail
+                                         (300, 264, 136, 0, 0), (264, 136, 100, 1, 0),
+                                         (520, 392, 200, 1, 1), (264, 520, 328, 0, 1)])
 def test_bgemm_ragged_and_partial_tiles(hk, orc, M, N, K, ta, tb):
     say("bgemm ragged", M, N, K, ta, tb)
     A, B, C0 = _operands(orc, M, N, K, ta, tb, 500)
