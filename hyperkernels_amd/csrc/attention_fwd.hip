@@ -15,10 +15,12 @@
 // plus a single cross-half shuffle, the rescale factor is per lane, and the exponentiated
 // scores are already laid out as the B operand of the next product, O^T += V^T P^T, which
 // keeps O^T per lane as well (no LDS round trip of P, no cross-lane gathers of the rescale).
-// Q stays in registers (pre-scaled by scale * log2 e, so the softmax uses exp2); K and V tiles
-// of 64 keys go through two LDS stages (rows padded to 68 floats: conflict-free fragment
-// reads) with the next tile's global loads in flight. Causal workgroups are launched heaviest
-// first and stop at the diagonal.
+// Q stays in registers (pre-scaled by scale * log2 e, so the softmax uses the hardware exp2); K
+// and V tiles of 32 keys go through two LDS stages, K as [key][d] and V transposed as [d][key]
+// (rows padded to 68 / 36 floats: conflict-free 16-byte fragment reads), with the next tile's
+// global loads in flight. 35 KB of LDS and <= 168 VGPRs per workgroup let 3 workgroups share a
+// CU, so the BASELINE grid (768 workgroups) runs in one round on 256 CUs. Causal workgroups are
+// launched heaviest first and stop at the diagonal.
 #include <mutex>
 
 #include "hk_device.h"
@@ -35,27 +37,37 @@ namespace {
 
 constexpr int kHD = 64;
 constexpr int kBQ = 128;                 // queries per workgroup (4 waves x 32)
-constexpr int kBKV = 64;                 // keys per K/V tile
-constexpr int kPitch = kHD + 4;          // LDS row pitch in floats
-constexpr int kTileFloats = kBKV * kPitch;
-constexpr size_t kLdsBytes = 2 * 2 * kTileFloats * sizeof(float);  // K and V, two stages
+constexpr int kBKV = 32;                 // keys per K/V tile
+constexpr int kKPitch = kHD + 4;         // K tile [key][d] row pitch (floats)
+constexpr int kVPitch = kBKV + 4;        // V^T tile [d][key] row pitch (floats)
+constexpr int kKFloats = kBKV * kKPitch;
+constexpr int kVFloats = kHD * kVPitch;
+constexpr int kStageFloats = kKFloats + kVFloats;
+constexpr size_t kLdsBytes = 2 * kStageFloats * sizeof(float);  // two stages, 35,840 bytes
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-// K/V tile loader: 64 rows x 64 floats = 1024 16-byte vectors per tensor; thread t moves vectors
-// t + 256 j (j = 0..3): 16 lanes cover one 256-byte row.
+// 2^x with the hardware exp2 (v_exp_f32, ~1 ulp). Arguments are scores minus a running max, so
+// they are <= 0; results below 2^-126 flush to zero, which only drops terms that are at most
+// 2^-126 of the row's largest one.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// K/V tile loader: 32 keys x 64 floats of each of K and V = 512 16-byte vectors per tensor;
+// thread t moves vectors t and t + 256 (key f / 16, d (f % 16) * 4). K is stored as it lies
+// ([key][d], pitch 68), V transposed ([d][key], pitch 36) so that the P V product reads four
+// consecutive keys of one d with one 16-byte LDS read.
 struct KVLoader {
   const float* k;
   const float* v;
   int64_t ks, vs;  // row strides (elements)
   int64_t T;
 
-  __device__ void load(int64_t k0, float4 (&rk)[4], float4 (&rv)[4]) const {
+  __device__ void load(int64_t k0, float4 (&rk)[2], float4 (&rv)[2]) const {
     const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       const int f = threadIdx.x + 256 * j;
       const int64_t row = k0 + (f >> 4);
       const int col = (f & 15) * 4;
@@ -63,21 +75,28 @@ struct KVLoader {
       rv[j] = row < T ? *reinterpret_cast<const float4*>(v + row * vs + col) : zero;
     }
   }
-  __device__ static void store(float* sk, float* sv, const float4 (&rk)[4], const float4 (&rv)[4]) {
+  __device__ static void store(float* st, const float4 (&rk)[2], const float4 (&rv)[2]) {
+    float* sk = st;
+    float* svt = st + kKFloats;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       const int f = threadIdx.x + 256 * j;
-      const int off = (f >> 4) * kPitch + (f & 15) * 4;
-      *reinterpret_cast<float4*>(sk + off) = rk[j];
-      *reinterpret_cast<float4*>(sv + off) = rv[j];
+      const int key = f >> 4, d = (f & 15) * 4;
+      *reinterpret_cast<float4*>(sk + key * kKPitch + d) = rk[j];
+      svt[(d + 0) * kVPitch + key] = rv[j].x;
+      svt[(d + 1) * kVPitch + key] = rv[j].y;
+      svt[(d + 2) * kVPitch + key] = rv[j].z;
+      svt[(d + 3) * kVPitch + key] = rv[j].w;
     }
   }
 };
 
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(hk_attn_fwd_params p) {
+// Per 32-key tile and wave (32 queries): S^T = K Q^T is one 32 x 32 accumulator block (32 MFMAs
+// over d), P^T = exp2(S^T - m) stays in that block's registers, and O^T += V^T P^T is two
+// blocks (d halves) of 16 MFMAs each. Accumulator element i of a lane (query c = lane % 32,
+// half hh = lane / 32) covers key 8 (i / 4) + 4 hh + i % 4 of the tile.
+__global__ __launch_bounds__(256, 3) void attn_fwd_kernel(hk_attn_fwd_params p) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  float* sK = lds;                       // [2][kTileFloats]
-  float* sV = lds + 2 * kTileFloats;     // [2][kTileFloats]
 
   const int64_t T = p.T;
   const int nqt = static_cast<int>((T + kBQ - 1) / kBQ);
@@ -116,10 +135,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(hk_attn_fwd_params p) 
   const int nkv = static_cast<int>((kv_end + kBKV - 1) / kBKV);
   KVLoader ld{p.K + b * p.k_strideB + h * p.k_strideH, p.V + b * p.v_strideB + h * p.v_strideH,
               p.k_strideM, p.v_strideM, T};
-  float4 rk[4], rv[4];
+  float4 rk[2], rv[2];
   if (nkv > 0) {
     ld.load(0, rk, rv);
-    KVLoader::store(sK, sV, rk, rv);
+    KVLoader::store(lds, rk, rv);
   }
   __syncthreads();
 
@@ -128,67 +147,69 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(hk_attn_fwd_params p) 
     const bool more = kt + 1 < nkv;
     if (more) ld.load(static_cast<int64_t>(kt + 1) * kBKV, rk, rv);
     const int64_t k0 = static_cast<int64_t>(kt) * kBKV;
-    const float* k_st = sK + cur * kTileFloats;
-    const float* v_st = sV + cur * kTileFloats;
+    const float* k_st = lds + cur * kStageFloats;
+    const float* vt_st = k_st + kKFloats;
     // a wave whose queries all precede this tile has nothing to add (causal)
     if (!p.is_causal || k0 <= q0w + 31) {
-      f32x16_t s[2] = {f32x16_t{}, f32x16_t{}};
+      f32x16_t s = f32x16_t{};
+      const float* krow = k_st + c * kKPitch + 32 * hh;
+      float4 kf[8];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const float* krow = k_st + (32 * kb + c) * kPitch + 32 * hh;
+      for (int j = 0; j < 8; ++j) kf[j] = *reinterpret_cast<const float4*>(krow + 4 * j);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float4 kf = *reinterpret_cast<const float4*>(krow + 4 * j);
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, qr[4 * j + 0], s[kb], 0, 0, 0);
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qr[4 * j + 1], s[kb], 0, 0, 0);
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qr[4 * j + 2], s[kb], 0, 0, 0);
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qr[4 * j + 3], s[kb], 0, 0, 0);
-        }
+      for (int j = 0; j < 8; ++j) {
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].x, qr[4 * j + 0], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].y, qr[4 * j + 1], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].z, qr[4 * j + 2], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].w, qr[4 * j + 3], s, 0, 0, 0);
       }
-      // mask (causal: key > query; any: key >= T), tile max over this query's 64 keys
-      float mt = -INFINITY;
-      const bool need_mask = (p.is_causal && k0 + kBKV - 1 > q0w) || k0 + kBKV > T;
+      // V^T operands of this tile: row d = 32 db + c, keys 8 g + 4 hh .. +3
+      float4 vf[2][4];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          vf[db][g] = *reinterpret_cast<const float4*>(vt_st + (32 * db + c) * kVPitch + 8 * g + 4 * hh);
+      // mask (causal: key > query; any: key >= T), tile max over this query's 32 keys
+      const bool need_mask = (p.is_causal && k0 + kBKV - 1 > q0w) || k0 + kBKV > T;
+      if (need_mask) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          if (need_mask) {
-            const int64_t key = k0 + 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
-            if (key >= T || (p.is_causal && key > q)) s[kb][i] = -INFINITY;
-          }
-          mt = fmaxf(mt, s[kb][i]);
+          const int64_t key = k0 + 8 * (i >> 2) + 4 * hh + (i & 3);
+          if (key >= T || (p.is_causal && key > q)) s[i] = -INFINITY;
         }
+      }
+      float mt = s[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mt = fmaxf(mt, s[i]);
       mt = fmaxf(mt, __shfl_xor(mt, 32, HK_WAVE));
       const float m_new = fmaxf(m, mt);
       // rows with nothing unmasked so far keep m = -inf and contribute nothing
-      const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m - m_new);
+      const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m - m_new);
       const float mref = (m_new == -INFINITY) ? 0.f : m_new;
       float ls = 0.f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float e = exp2f(s[kb][i] - mref);
-          s[kb][i] = e;
-          ls += e;
-        }
+      for (int i = 0; i < 16; ++i) {
+        const float e = fast_exp2(s[i] - mref);
+        s[i] = e;
+        ls += e;
+      }
       l = l * alpha + ls;
       m = m_new;
 #pragma unroll
       for (int db = 0; db < 2; ++db) o[db] *= alpha;
-      // O^T[d][q] += sum_key V[key][d] P^T[key][q]
+      // O^T[d][q] += sum_key V^T[d][key] P^T[key][q]
 #pragma unroll
-      for (int db = 0; db < 2; ++db)
+      for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
-            const float vv = v_st[key * kPitch + 32 * db + c];
-            o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, s[kb][i], o[db], 0, 0, 0);
-          }
+        for (int db = 0; db < 2; ++db) {
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[db][g].x, s[4 * g + 0], o[db], 0, 0, 0);
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[db][g].y, s[4 * g + 1], o[db], 0, 0, 0);
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[db][g].z, s[4 * g + 2], o[db], 0, 0, 0);
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[db][g].w, s[4 * g + 3], o[db], 0, 0, 0);
+        }
     }
-    if (more) KVLoader::store(sK + (cur ^ 1) * kTileFloats, sV + (cur ^ 1) * kTileFloats, rk, rv);
+    if (more) KVLoader::store(lds + (cur ^ 1) * kStageFloats, rk, rv);
     __syncthreads();
   }
 
