@@ -19,8 +19,8 @@
 // and V tiles of 32 keys go through two LDS stages, K as [key][d] and V transposed as [d][key]
 // (rows padded to 68 / 36 floats: conflict-free 16-byte fragment reads), with the next tile's
 // global loads in flight. 35 KB of LDS and <= 168 VGPRs per workgroup let 3 workgroups share a
-// CU, so the BASELINE grid (768 workgroups) runs in one round on 256 CUs. Causal workgroups are
-// launched heaviest first and stop at the diagonal.
+// CU, so the BASELINE grid (768 workgroups) runs in one round on 256 CUs. Causal workgroups stop
+// at the diagonal; their order is described at snake_item.
 #include <mutex>
 
 #include "hk_device.h"
@@ -95,13 +95,27 @@ struct KVLoader {
 // over d), P^T = exp2(S^T - m) stays in that block's registers, and O^T += V^T P^T is two
 // blocks (d halves) of 16 MFMAs each. Accumulator element i of a lane (query c = lane % 32,
 // half hh = lane / 32) covers key 8 (i / 4) + 4 hh + i % 4 of the tile.
-__global__ __launch_bounds__(256, 3) void attn_fwd_kernel(hk_attn_fwd_params p) {
+// Work order. Workgroup L of the 1-D grid gets item snake(L): with P = number of CUs, round
+// r = L / P is traversed forwards for even r and backwards for odd r (a boustrophedon). Items
+// are numbered heaviest first (under causal masking q-tile nqt-1 of every (batch, head) first,
+// then q-tile nqt-2, ...). When the whole grid is resident at once and the dispatcher places
+// workgroup L on CU L % P, CU j receives items j, 2P-1-j, 2P+j, ...: heavy, light, heavy...,
+// which evens out the per-CU sums; any placement still computes every item exactly once.
+__device__ __forceinline__ int snake_item(int L, int n, int P) {
+  const int r = L / P, j = L - r * P;
+  if ((r & 1) == 0) return L;
+  const int m = min(P, n - r * P);  // items in this round
+  return r * P + (m - 1 - j);
+}
+
+__global__ __launch_bounds__(256, 3) void attn_fwd_kernel(hk_attn_fwd_params p, int nbh, int ncu) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
 
   const int64_t T = p.T;
   const int nqt = static_cast<int>((T + kBQ - 1) / kBQ);
-  const int qt = p.is_causal ? (nqt - 1 - static_cast<int>(blockIdx.x)) : static_cast<int>(blockIdx.x);
-  const int bh = blockIdx.y;
+  const int item = snake_item(static_cast<int>(blockIdx.x), nqt * nbh, ncu);
+  const int qt = nqt - 1 - item / nbh;
+  const int bh = item - (nqt - 1 - qt) * nbh;
   const int b = bh / p.nh, h = bh - b * p.nh;
   const float* Qb = p.Q + b * p.q_strideB + h * p.q_strideH;
   float* Ob = p.O + b * p.o_strideB + h * p.o_strideH;
@@ -275,7 +289,7 @@ extern "C" hipError_t hk_fused_attn_forward(const hk_attn_fwd_params* params, in
                rows_aligned(p.O, p.o_strideB, p.o_strideH, p.o_strideM));
   const int64_t bh = static_cast<int64_t>(p.B) * p.nh;
   const int64_t nqt = (p.T + kBQ - 1) / kBQ;
-  HK_CHECK_ARG(bh <= 65535 && nqt <= INT32_MAX);
+  HK_CHECK_ARG(bh * nqt <= INT32_MAX);
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
@@ -284,8 +298,8 @@ extern "C" hipError_t hk_fused_attn_forward(const hk_attn_fwd_params* params, in
                                static_cast<int>(kLdsBytes));
   });
   HK_RETURN_IF_ERROR(attr);
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3(static_cast<unsigned>(nqt), static_cast<unsigned>(bh)),
-                     dim3(256), kLdsBytes, stream, p);
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3(static_cast<unsigned>(nqt * bh)), dim3(256),
+                     kLdsBytes, stream, p, static_cast<int>(bh), hk::device_cu_count());
   return hk::launch_status();
 }
 
