@@ -17,11 +17,13 @@
 //
 // Design (gfx950): the same tiling as the BF16 GEMM of this library - 256 x 256 workgroup
 // tile, 4 waves of 128 x 128 (4 x 4 MFMA tiles, 256 fp32 accumulators per lane), k-tiles of
-// 32 fp32 (128-byte LDS rows, chunks XOR-permuted so fragment reads and stores are free of
-// bank conflicts), two LDS stages with the next k-tile's loads in flight. An operand
-// that is M/N-contiguous in HBM is read as 8 k-rows x 4 values and transposed in registers.
-// Lane (r, h) of a wave feeds k = 16h + s of each 32-deep k-tile at step s, so a lane reads 16
-// consecutive k values of its row per tile as four 16-byte LDS loads.
+// 32 fp32 copied HBM/L2 -> LDS without passing through registers (global_load_lds_dwordx4)
+// into a 2-stage LDS ring, one barrier per k-tile. K-major operands sit in LDS as [row][k]
+// (read 4 k at a time with 16-byte reads), M/N-major ones as [k][row] like in HBM (one float
+// per lane and MFMA step, 128 contiguous bytes per half-wave), so no layout is transposed in
+// registers. Lane (r, h) of a wave feeds k = 16h + s of each 32-deep k-tile at step s.
+// The epilogue writes straight from registers: with the MFMA inputs swapped each lane holds 4
+// consecutive columns of one output row per accumulator quad (one 16-byte store).
 // Split-K: every split writes fp32 partials; a second kernel sums them in split order and
 // applies alpha, beta and the bias exactly once (deterministic, and the bias is not repeated
 // per split as in the reference's atomics).
@@ -33,83 +35,64 @@
 namespace {
 
 constexpr int BM = 256, BN = 256, BK = 32;
+constexpr int kStages = 2;                             // LDS ring depth (k-tiles)
 constexpr int kThreads = 256;
 constexpr int kWave = 128;
-constexpr int kTileElems = 256 * BK;                  // one operand stage, floats
-constexpr int kStagePitch = 128 + 4;
-constexpr size_t kLdsMain = 2 * 2 * kTileElems * sizeof(float);                    // 131072
-constexpr size_t kLdsEpi = static_cast<size_t>(BM) * kStagePitch * sizeof(float);   // 135168
-constexpr size_t kLdsBytes = kLdsMain > kLdsEpi ? kLdsMain : kLdsEpi;
+constexpr int kStageBytes = 256 * BK * 4;              // one operand, one k-tile (32 KiB)
+constexpr int kLoadsPerWave = kStageBytes / 1024 / 4;  // 16-byte lane copies per operand per wave
+constexpr size_t kLdsBytes = static_cast<size_t>(kStages) * 2 * kStageBytes;  // 128 KiB
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+#define HK_LDS __attribute__((address_space(3)))
 
-// Same placement as the BF16 GEMM: 128-byte rows, 16-byte chunk c of row r at c ^ f(r),
-// f(r) = (r ^ (r >> 3)) & 7, conflict-free for 8 consecutive rows at one chunk, for one row at
-// 8 chunks and for the transposed stores (rows 4l + c, l = 0..7). Returns the offset in floats.
-__device__ __forceinline__ int lds_off(int row, int chunk) {
-  return row * 32 + ((chunk ^ ((row ^ (row >> 3)) & 7)) * 4);
+// 16-byte global -> LDS copy of one lane (global_load_lds_dwordx4); the wave's 64 lanes write
+// 1 KiB at m0 + 16 * lane. Inline asm so that the compiler does not make every later LDS read
+// wait for all outstanding copies (the kernel orders them itself with vmcnt + barrier).
+// Address = sbase (wave-uniform 64-bit) + voff (per-lane byte offset).
+__device__ __forceinline__ void copy16_to_lds(const void* sbase, int voff, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+               "s"(lds_addr));
 }
 
-// One operand's share of a k-tile (256 rows x 32 k fp32), 8 16-byte loads per thread.
-// KMAJOR: element (row, k) at base[row * ld + k]; thread tt loads chunk tt % 8 of rows
-//   tt / 8 + 32 j.
-// otherwise: element at base[k * ld + row]; thread tt owns rows 4 (tt % 64) .. +4 and k-rows
-//   8 (tt / 64) .. +8 (64 lanes read 1 KB contiguous per k-row), transposed in registers into
-//   4 rows x 2 chunks.
+// One operand of a k-tile in LDS: 256 rows of M (or N) by BK = 32 k, fp32, 32 KiB.
+//
+// K-major operands (element (row, k) at base[row * ld + k]) are stored [row][32 k]: 128-byte
+// rows whose 16-byte chunks (4 k each) sit at chunk ^ (row & 7); a copy instruction moves 8
+// rows (lane l: row l / 8, stored chunk l % 8), 8 lanes per 128-byte HBM row segment. Lane
+// (r, h) of a wave feeds k = 16 h + s of the tile at MFMA step s, so it reads 16 consecutive k
+// of its row as four 16-byte LDS reads (chunks 4 h .. 4 h + 3); 8 consecutive rows at one chunk
+// position cover all 32 banks once.
+// M/N-major operands (element at base[k * ld + row]) are stored as in HBM, [32 k][256 rows]
+// (1 KiB per k-row, one copy instruction); the operand of MFMA step s is one float per lane,
+// row k = 16 h + s, 32 consecutive rows per half-wave (all 32 banks).
 template <bool KMAJOR>
-struct TileLoader {
-  const float* base;
-  int64_t ld;
-  int rows, K, rbase, tt;
-
-  __device__ void init(const float* b, int64_t l, int nrows, int k, int tile_row0, int t) {
-    base = b;
-    ld = l;
-    rows = nrows;
-    K = k;
-    rbase = tile_row0;
-    tt = t;
-  }
-
-  __device__ void load(int k0, float4 (&reg)[8]) const {
-    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+struct TileOperand {
+  __device__ static void source(int ii, int lane, int& row, int& k) {
     if (KMAJOR) {
-      const int k = k0 + (tt & 7) * 4;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int r = rbase + (tt >> 3) + 32 * j;
-        reg[j] = (r < rows && k < K)
-                     ? *reinterpret_cast<const float4*>(base + static_cast<int64_t>(r) * ld + k)
-                     : zero;
-      }
+      row = ii * 8 + (lane >> 3);
+      k = ((lane & 7) ^ (row & 7)) * 4;
     } else {
-      const int r = rbase + (tt & 63) * 4;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int k = k0 + (tt >> 6) * 8 + j;
-        reg[j] = (r < rows && k < K)
-                     ? *reinterpret_cast<const float4*>(base + static_cast<int64_t>(k) * ld + r)
-                     : zero;
-      }
+      k = ii;
+      row = lane * 4;
     }
   }
-
-  __device__ void store(float* stage, const float4 (&reg)[8]) const {
+  __device__ static int64_t byte_offset(int row, int k, int64_t ld) {
+    return KMAJOR ? 4 * (static_cast<int64_t>(row) * ld + k)
+                  : 4 * (static_cast<int64_t>(k) * ld + row);
+  }
+  __device__ static int64_t ktile_step(int64_t ld) { return KMAJOR ? BK : BK * ld; }
+  // Operands of MFMA steps 4 qd .. 4 qd + 3 for MFMA block b (32 rows at wave offset wo).
+  __device__ static f32x4_t read(const unsigned char HK_LDS* st, int wo, int b, int qd,
+                                 int lane) {
+    const int r = wo + b * 32 + (lane & 31), h = lane >> 5;
     if (KMAJOR) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        *reinterpret_cast<float4*>(stage + lds_off((tt >> 3) + 32 * j, tt & 7)) = reg[j];
+      const int c = 4 * h + qd;
+      return *reinterpret_cast<const f32x4_t HK_LDS*>(st + r * 128 + ((c ^ (r & 7)) * 16));
     } else {
-      const int row0 = (tt & 63) * 4;
-      const int ch0 = (tt >> 6) * 2;
-      const float* v = reinterpret_cast<const float*>(reg);  // v[k * 4 + c]
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        *reinterpret_cast<float4*>(stage + lds_off(row0 + c, ch0)) =
-            make_float4(v[0 * 4 + c], v[1 * 4 + c], v[2 * 4 + c], v[3 * 4 + c]);
-        *reinterpret_cast<float4*>(stage + lds_off(row0 + c, ch0 + 1)) =
-            make_float4(v[4 * 4 + c], v[5 * 4 + c], v[6 * 4 + c], v[7 * 4 + c]);
-      }
+      const float HK_LDS* col =
+          reinterpret_cast<const float HK_LDS*>(st) + (16 * h + 4 * qd) * 256 + r;
+      return f32x4_t{col[0], col[256], col[512], col[768]};
     }
   }
 };
@@ -128,34 +111,6 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
   tn = in_group / gsz;
 }
 
-__device__ __forceinline__ void mma_stage(const float* a_st, const float* b_st, int wm, int wn,
-                                          int lane, f32x16_t (&acc)[4][4]) {
-  const int frow = lane & 31;
-  const int half = lane >> 5;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    float4 af[4], bfr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      af[i] = *reinterpret_cast<const float4*>(a_st + lds_off(wm * kWave + i * 32 + frow,
-                                                              half * 4 + q));
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      bfr[j] = *reinterpret_cast<const float4*>(b_st + lds_off(wn * kWave + j * 32 + frow,
-                                                               half * 4 + q));
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float a = e == 0 ? af[i].x : e == 1 ? af[i].y : e == 2 ? af[i].z : af[i].w;
-          const float b = e == 0 ? bfr[j].x : e == 1 ? bfr[j].y : e == 2 ? bfr[j].z : bfr[j].w;
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i][j], 0, 0, 0);
-        }
-  }
-}
-
 struct Epilogue {
   float alpha, beta;
   const float* bias;
@@ -172,14 +127,36 @@ __device__ __forceinline__ float bias_at(const Epilogue& ep, int M, int N, int b
   return 0.f;
 }
 
+__device__ __forceinline__ float f4_get(const f32x4_t& v, int e) { return v[e]; }
+
+// 16 MFMAs (4 x 4 blocks) of one k step; B block as the MFMA "A" input so that each lane ends
+// up holding 4 consecutive output columns of one output row per accumulator quad.
+__device__ __forceinline__ void mma_quad(const f32x4_t (&af)[4], const f32x4_t (&bf)[4],
+                                         f32x16_t (&acc)[4][4]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4_get(bf[j], e), f4_get(af[i], e),
+                                                         acc[i][j], 0, 0, 0);
+}
+
+// Main loop per k-tile kt (ring slot kt % 2) in 4 quads of 4 MFMA steps (64 MFMAs each):
+// quads 0-2 read the operands of the next quad while multiplying; quad 3 waits for this
+// wave's copies of tile kt + 1, takes the barrier, reads quad 0 of tile kt + 1 and issues the
+// copies of tile kt + 2 into slot kt % 2 between its MFMAs.
 template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL>
 __global__ __launch_bounds__(kThreads, 1) void sgemm_tiled(
     int M, int N, int K, const float* __restrict__ A, int64_t lda, int64_t sA,
     const float* __restrict__ B, int64_t ldb, int64_t sB, float* __restrict__ C, int64_t ldc,
     int64_t sC, Epilogue ep, int split_k, int k_per_split, float* __restrict__ part) {
+  using OA = TileOperand<A_KMAJOR>;
+  using OB = TileOperand<B_KMAJOR>;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
-  float* sA_st = reinterpret_cast<float*>(lds_raw);
-  float* sB_st = sA_st + 2 * kTileElems;
+  unsigned char HK_LDS* ldsA = (unsigned char HK_LDS*)lds_raw;
+  unsigned char HK_LDS* ldsB = ldsA + kStages * kStageBytes;
 
   const int batch = blockIdx.z / split_k;
   const int split = blockIdx.z - batch * split_k;
@@ -188,17 +165,57 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_tiled(
   tile_coords(tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int kbeg = split * k_per_split;
-  const int kend = min(K, kbeg + k_per_split);
+  const int klen = min(K, kbeg + k_per_split) - kbeg;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  TileLoader<A_KMAJOR> la;
-  TileLoader<B_KMAJOR> lb;
-  la.init(A + static_cast<int64_t>(batch) * sA, lda, M, kend, m0, tid);
-  lb.init(B + static_cast<int64_t>(batch) * sB, ldb, N, kend, n0, tid);
+  // Rows past M (N) are read clamped (their outputs are not stored); k past the split's end is
+  // zero-filled on the last k-tile.
+  const unsigned char* gA = reinterpret_cast<const unsigned char*>(
+      A + static_cast<int64_t>(batch) * sA +
+      (A_KMAJOR ? static_cast<int64_t>(m0) * lda + kbeg : static_cast<int64_t>(kbeg) * lda + m0));
+  const unsigned char* gB = reinterpret_cast<const unsigned char*>(
+      B + static_cast<int64_t>(batch) * sB +
+      (B_KMAJOR ? static_cast<int64_t>(n0) * ldb + kbeg : static_cast<int64_t>(kbeg) * ldb + n0));
+  int offA[kLoadsPerWave], offB[kLoadsPerWave], kA[kLoadsPerWave], kB[kLoadsPerWave];
+#pragma unroll
+  for (int i = 0; i < kLoadsPerWave; ++i) {
+    int row, k;
+    OA::source(wave * kLoadsPerWave + i, lane, row, k);
+    row = min(row, (A_KMAJOR ? M - 1 : M - 4) - m0);
+    offA[i] = static_cast<int>(OA::byte_offset(row, k, lda));
+    kA[i] = k;
+    OB::source(wave * kLoadsPerWave + i, lane, row, k);
+    row = min(row, (B_KMAJOR ? N - 1 : N - 4) - n0);
+    offB[i] = static_cast<int>(OB::byte_offset(row, k, ldb));
+    kB[i] = k;
+  }
+  const int64_t stepA = 4 * OA::ktile_step(lda), stepB = 4 * OB::ktile_step(ldb);
+  const unsigned ldsA_addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(ldsA));
+  const unsigned ldsB_addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(ldsB));
+  const int ktiles = (klen + BK - 1) / BK;
+  const bool tail = (klen % BK) != 0;
+
+  auto copy = [&](int kt, int slot, int q, bool fill) {
+    const bool isA = q < kLoadsPerWave;
+    const int i = isA ? q : q - kLoadsPerWave;
+    const unsigned char* base = (isA ? gA + kt * stepA : gB + kt * stepB);
+    const int off = isA ? offA[i] : offB[i];
+    const unsigned lds = (isA ? ldsA_addr : ldsB_addr) + slot * kStageBytes +
+                         (wave * kLoadsPerWave + i) * 1024;
+    if (!fill) {
+      copy16_to_lds(base, off, lds);
+    } else if (kt * BK + (isA ? kA[i] : kB[i]) < klen) {
+      copy16_to_lds(base, off, lds);
+    } else {
+      typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+      *reinterpret_cast<u32x4_t HK_LDS*>((unsigned char HK_LDS*)(uintptr_t)lds + 16 * lane) =
+          u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  constexpr int kCopies = 2 * kLoadsPerWave;
 
   f32x16_t acc[4][4];
 #pragma unroll
@@ -206,90 +223,119 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_tiled(
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
 
-  float4 ra[8], rb[8];
-  const int ktiles = (kend - kbeg + BK - 1) / BK;
+#pragma unroll
+  for (int p = 0; p < kStages; ++p)
+    if (p < ktiles) {
+      const bool fill = tail && p == ktiles - 1;
+#pragma unroll
+      for (int q = 0; q < kCopies; ++q) copy(p, p, q, fill);
+    }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+
+  f32x4_t fa[2][4], fb[2][4];
   if (ktiles > 0) {
-    la.load(kbeg, ra);
-    lb.load(kbeg, rb);
-    la.store(sA_st, ra);
-    lb.store(sB_st, rb);
-  }
-  __syncthreads();
-  for (int kt = 0; kt < ktiles; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < ktiles;
-    if (more) {
-      la.load(kbeg + (kt + 1) * BK, ra);
-      lb.load(kbeg + (kt + 1) * BK, rb);
-    }
-    mma_stage(sA_st + cur * kTileElems, sB_st + cur * kTileElems, wm, wn, lane, acc);
-    if (more) {
-      la.store(sA_st + (cur ^ 1) * kTileElems, ra);
-      lb.store(sB_st + (cur ^ 1) * kTileElems, rb);
-    }
-    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[0][i] = OA::read(ldsA, wm * kWave, i, 0, lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fb[0][j] = OB::read(ldsB, wn * kWave, j, 0, lane);
   }
 
-  const int lrow = 4 * (lane >> 5);
-  const int lcol = lane & 31;
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int slot = kt & 1;
+    const unsigned char HK_LDS* sa = ldsA + slot * kStageBytes;
+    const unsigned char HK_LDS* sb = ldsB + slot * kStageBytes;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int cur = qd & 1, nxt = cur ^ 1;
+      if (qd + 1 < 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fa[nxt][i] = OA::read(sa, wm * kWave, i, qd + 1, lane);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fb[nxt][j] = OB::read(sb, wn * kWave, j, qd + 1, lane);
+        mma_quad(fa[cur], fb[cur], acc);
+      } else {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        if (kt + 1 < ktiles) {
+          const unsigned char HK_LDS* na = ldsA + (slot ^ 1) * kStageBytes;
+          const unsigned char HK_LDS* nb = ldsB + (slot ^ 1) * kStageBytes;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) fa[nxt][i] = OA::read(na, wm * kWave, i, 0, lane);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) fb[nxt][j] = OB::read(nb, wn * kWave, j, 0, lane);
+        }
+        const bool more = kt + kStages < ktiles;
+        const bool fill = tail && kt + kStages == ktiles - 1;
+        // 64 MFMAs with the 16 copies of tile kt + 2 spread between them
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                  f4_get(fb[cur][j], e), f4_get(fa[cur][i], e), acc[i][j], 0, 0, 0);
+              const int q = (e * 16 + i * 4 + j);
+              if (more && (q & 3) == 0 && (q >> 2) < kCopies) copy(kt + kStages, slot, q >> 2, fill);
+            }
+      }
+    }
+  }
+
+  // Epilogue. Lane l holds, for MFMA block (i, j) and quad q, output row
+  // wm*128 + 32 i + l % 32 and columns wn*128 + 32 j + 8 q + 4 (l / 32) .. +3.
+  const int row0 = m0 + wm * kWave + (lane & 31);
+  const int col0 = n0 + wn * kWave + 4 * (lane >> 5);
   if (PARTIAL) {
     float* out = part + (static_cast<int64_t>(split) * (gridDim.z / split_k) + batch) *
                             static_cast<int64_t>(M) * N;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
+      const int row = row0 + 32 * i;
+      if (row >= M) continue;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * kWave + i * 32 + 8 * (r >> 2) + lrow + (r & 3);
-          const int col = n0 + wn * kWave + j * 32 + lcol;
-          if (row < M && col < N) out[static_cast<int64_t>(row) * N + col] = acc[i][j][r];
+        for (int q = 0; q < 4; ++q) {
+          const int col = col0 + 32 * j + 8 * q;
+          if (col < N)
+            *reinterpret_cast<float4*>(out + static_cast<int64_t>(row) * N + col) =
+                make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                            acc[i][j][4 * q + 3]);
         }
+    }
     return;
   }
-
-  float* stage = reinterpret_cast<float*>(lds_raw);
   float* Cb = C + static_cast<int64_t>(batch) * sC;
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    if (wn == half) {
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + 32 * i;
+    if (row >= M) continue;
+    float* crow = Cb + static_cast<int64_t>(row) * ldc;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+      for (int q = 0; q < 4; ++q) {
+        const int col = col0 + 32 * j + 8 * q;
+        if (col >= N) continue;
+        float f[4];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int row = wm * kWave + i * 32 + 8 * (r >> 2) + lrow + (r & 3);
-            stage[row * kStagePitch + j * 32 + lcol] = acc[i][j][r];
-          }
-    }
-    __syncthreads();
-#pragma unroll 4
-    for (int it = 0; it < 32; ++it) {
-      const int q = tid + it * kThreads;
-      const int row = q >> 5;
-      const int c4 = (q & 31) * 4;
-      const int grow = m0 + row;
-      const int gcol = n0 + half * 128 + c4;
-      if (grow < M && gcol < N) {
-        const float4 v = *reinterpret_cast<const float4*>(stage + row * kStagePitch + c4);
-        float4* dst = reinterpret_cast<float4*>(Cb + static_cast<int64_t>(grow) * ldc + gcol);
-        float f[4] = {v.x, v.y, v.z, v.w};
-        float old[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int e = 0; e < 4; ++e) f[e] = ep.alpha * acc[i][j][4 * q + e];
+        float4* dst = reinterpret_cast<float4*>(crow + col);
         if (ep.beta != 0.0f) {
           const float4 o = *dst;
-          old[0] = o.x; old[1] = o.y; old[2] = o.z; old[3] = o.w;
+          f[0] += ep.beta * o.x;
+          f[1] += ep.beta * o.y;
+          f[2] += ep.beta * o.z;
+          f[3] += ep.beta * o.w;
         }
+        if (ep.bias) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          f[e] = ep.alpha * f[e];
-          if (ep.beta != 0.0f) f[e] += ep.beta * old[e];
-          if (ep.bias) f[e] += ep.bias_scale * bias_at(ep, M, N, batch, gcol + e);
+          for (int e = 0; e < 4; ++e) f[e] += ep.bias_scale * bias_at(ep, M, N, batch, col + e);
         }
         *dst = make_float4(f[0], f[1], f[2], f[3]);
       }
-    }
-    __syncthreads();
   }
 }
 
@@ -393,7 +439,9 @@ hipError_t sgemm_run(bool ta, bool tb, int M, int N, int K, float alpha, const f
   const bool tiled_ok = (contig_a % 4 == 0) && (contig_b % 4 == 0) && (N % 4 == 0) &&
                         (lda % 4 == 0) && (ldb % 4 == 0) && (ldc % 4 == 0) &&
                         (strideA % 4 == 0) && (strideB % 4 == 0) && (strideC % 4 == 0) &&
-                        hk::aligned16(A) && hk::aligned16(B) && hk::aligned16(C) && K > 0;
+                        hk::aligned16(A) && hk::aligned16(B) && hk::aligned16(C) && K > 0 &&
+                        // per-lane source offsets inside a tile are 32-bit byte offsets
+                        lda < (1 << 21) && ldb < (1 << 21);
   if (!tiled_ok) {
     dim3 grid((N + 15) / 16, (M + 15) / 16, batchCount);
     hipLaunchKernelGGL(sgemm_simple, grid, dim3(256), 0, stream, ta ? 1 : 0, tb ? 1 : 0, M, N, K,
