@@ -379,18 +379,33 @@ __global__ __launch_bounds__(256) void bgemm_splitk_finalize(const float* __rest
                                                              float alpha, float beta,
                                                              uint16_t* __restrict__ C,
                                                              int64_t ldc, int64_t sC) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  // 4 consecutive outputs per thread (N is a multiple of 8 on the tiled path)
+  const int64_t idx = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
   const int64_t mn = static_cast<int64_t>(M) * N;
   if (idx >= mn * batch) return;
   const int b = static_cast<int>(idx / mn);
   const int64_t e = idx - b * mn;
   const int row = static_cast<int>(e / N), col = static_cast<int>(e - static_cast<int64_t>(row) * N);
-  float s = 0.f;
-  for (int k = 0; k < split_k; ++k) s += part[(static_cast<int64_t>(k) * batch + b) * mn + e];
-  uint16_t* dst = C + b * sC + static_cast<int64_t>(row) * ldc + col;
-  float f = alpha * s;
-  if (beta != 0.0f) f += beta * hk::bf16_to_f32(*dst);
-  *dst = hk::f32_to_bf16(f);
+  f32x2_t lo = f32x2_t{0.f, 0.f}, hi = f32x2_t{0.f, 0.f};
+  for (int k = 0; k < split_k; ++k) {
+    const float4 v = *reinterpret_cast<const float4*>(part + (static_cast<int64_t>(k) * batch + b) * mn + e);
+    lo += f32x2_t{v.x, v.y};
+    hi += f32x2_t{v.z, v.w};
+  }
+  lo *= alpha;
+  hi *= alpha;
+  uint2* dst = reinterpret_cast<uint2*>(C + b * sC + static_cast<int64_t>(row) * ldc + col);
+  if (beta != 0.0f) {
+    const uint2 old = *dst;
+    lo += beta * f32x2_t{__uint_as_float(old.x << 16), __uint_as_float(old.x & 0xffff0000u)};
+    hi += beta * f32x2_t{__uint_as_float(old.y << 16), __uint_as_float(old.y & 0xffff0000u)};
+  }
+  const bf16x2_t blo = __builtin_convertvector(lo, bf16x2_t);
+  const bf16x2_t bhi = __builtin_convertvector(hi, bf16x2_t);
+  uint2 v;
+  __builtin_memcpy(&v.x, &blo, 4);
+  __builtin_memcpy(&v.y, &bhi, 4);
+  *dst = v;
 }
 
 // Fallback: one thread per output, fp32 accumulation in k order.
@@ -465,12 +480,35 @@ hipError_t dispatch_layout(bool ta, bool tb, dim3 grid, hipStream_t stream, int 
                                       C, ldc, sC, split_k, kps, part);
 }
 
+// Split-K chosen by the library when the caller gives none: the split that minimises a simple
+// cost model of (rounds of 256 x 256 tiles over the CUs) x (k-tiles per split) plus the HBM
+// traffic of fp32 partials (written, then read back with one bf16 write by the finalize).
+// Few output tiles with a long K (e.g. the dB = X^T dY product, 100 tiles, 128 k-tiles) gain
+// most; the costs are per k-tile of one workgroup (~2.7 us) and ~5 TB/s for the partials.
+int auto_split_k(int64_t work_tiles, int64_t ktiles, int64_t outputs) {
+  const int64_t cus = hk::device_cu_count();
+  double best = 0.0;
+  int best_s = 1;
+  for (int s = 1; s <= 8; ++s) {
+    if (s > 1 && ktiles / s < 4) break;
+    const double rounds = static_cast<double>(hk::ceil_div(work_tiles * s, cus));
+    double cost = rounds * static_cast<double>(hk::ceil_div(ktiles, static_cast<int64_t>(s))) * 2.7;
+    if (s > 1) cost += static_cast<double>(8 * s + 2) * static_cast<double>(outputs) / 5.0e6;
+    if (s == 1 || cost < best) {
+      best = cost;
+      best_s = s;
+    }
+  }
+  return best_s;
+}
+
 hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_bits,
                      const hk_bf16* A, int lda, long long strideA, const hk_bf16* B, int ldb,
                      long long strideB, hk_bf16 beta_bits, hk_bf16* C, int ldc, long long strideC,
                      int batchCount, int splitK, hipStream_t stream) {
   HK_CHECK_ARG(transA >= 0 && transA <= 2 && transB >= 0 && transB <= 2);
-  HK_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batchCount >= 0 && splitK >= 1);
+  // splitK == 0: the library picks the split (auto_split_k)
+  HK_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batchCount >= 0 && splitK >= 0);
   if (M == 0 || N == 0 || batchCount == 0) return hipSuccess;
   HK_CHECK_ARG(C != nullptr && ldc >= N);
   const bool ta = transA != 0, tb = transB != 0;  // OP_C is OP_T for real bf16
@@ -496,6 +534,8 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
     return hk::launch_status();
   }
   const int64_t tiles = static_cast<int64_t>((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  if (splitK == 0) splitK = auto_split_k(tiles * batchCount, hk::ceil_div(K, BK),
+                                         static_cast<int64_t>(M) * N * batchCount);
   HK_CHECK_ARG(tiles <= INT32_MAX && static_cast<int64_t>(batchCount) * splitK <= 65535);
   if (splitK == 1) {
     dim3 grid(static_cast<unsigned>(tiles), 1, batchCount);
@@ -514,7 +554,7 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
                                            B, ldb, strideB, beta, C, ldc, strideC, used, kps,
                                            part));
   const int64_t total = static_cast<int64_t>(M) * N * batchCount;
-  hipLaunchKernelGGL(bgemm_splitk_finalize, dim3(static_cast<unsigned>(hk::ceil_div(total, 256))),
+  hipLaunchKernelGGL(bgemm_splitk_finalize, dim3(static_cast<unsigned>(hk::ceil_div(total, 1024))),
                      dim3(256), 0, stream, part, used, batchCount, M, N, alpha, beta, C,
                      static_cast<int64_t>(ldc), static_cast<int64_t>(strideC));
   return hk::launch_status();
@@ -527,7 +567,7 @@ extern "C" hipError_t hk_bgemm(int transA, int transB, int M, int N, int K, hk_b
                                int ldb, long long strideB, hk_bf16 beta, hk_bf16* C, int ldc,
                                long long strideC, int batchCount, hipStream_t stream) {
   return bgemm_run(transA, transB, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, C, ldc,
-                   strideC, batchCount, 1, stream);
+                   strideC, batchCount, 0, stream);
 }
 
 extern "C" hipError_t hk_bgemm_core(int layout, int splitK, int M, int N, int K, hk_bf16 alpha,
@@ -537,6 +577,7 @@ extern "C" hipError_t hk_bgemm_core(int layout, int splitK, int M, int N, int K,
                                     hipStream_t stream) {
   // BgemmLayout { NT, TN, NN } (blas/bf16/bgemm_core_template.cu:59)
   HK_CHECK_ARG(layout >= HK_LAYOUT_NT && layout <= HK_LAYOUT_NN);
+  HK_CHECK_ARG(splitK >= 1);
   const int ta = layout == HK_LAYOUT_TN ? 1 : 0;
   const int tb = layout == HK_LAYOUT_NT ? 1 : 0;
   return bgemm_run(ta, tb, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, C, ldc,
@@ -549,7 +590,7 @@ extern "C" hipError_t hk_bgemm_nt_backward(int M, int N, int K, hk_bf16 alpha, c
                                            long long strideC, int batchCount,
                                            hipStream_t stream) {
   return bgemm_run(0, 1, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, C, ldc, strideC,
-                   batchCount, 1, stream);
+                   batchCount, 0, stream);
 }
 
 extern "C" hipError_t hk_bgemm_tn_backward(int M, int N, int K, hk_bf16 alpha, const hk_bf16* A,
@@ -558,5 +599,5 @@ extern "C" hipError_t hk_bgemm_tn_backward(int M, int N, int K, hk_bf16 alpha, c
                                            long long strideC, int batchCount,
                                            hipStream_t stream) {
   return bgemm_run(1, 0, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, C, ldc, strideC,
-                   batchCount, 1, stream);
+                   batchCount, 0, stream);
 }

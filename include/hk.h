@@ -204,6 +204,9 @@ HK_API hipError_t hk_reduce_generic_f32(const float* src, float* dst, int out_nd
  * hk_bgemm_nt_backward (dA = dY * B^T) replaces bgemm_nt_backward_kernel
  *   (blas/bf16/bgemm_backward_nt_sm89_kernel.cu:23-32); hk_bgemm_tn_backward (dB = A^T * dY)
  *   replaces bgemm_tn_backward_kernel (blas/bf16/bgemm_backward_tn_sm89_kernel.cu:25-34).
+ * hk_bgemm and the two backward entry points have no split argument (as in the reference); the
+ *   library splits K itself when the output has too few 256 x 256 tiles to fill the device
+ *   (same fp32 partials and split-order sum as hk_bgemm_core).
  * Any M, N, K; the MFMA path needs the contiguous extents, leading dimensions and strides to
  * be multiples of 8 and 16-byte aligned pointers (the reference's own precondition,
  * bgemm_test.cu:252-256); other shapes run on a slower fp32-accumulating kernel.
