@@ -547,7 +547,7 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
   const int used = static_cast<int>(hk::ceil_div(K, kps));
   void* ws = nullptr;
   const size_t part_bytes = static_cast<size_t>(used) * batchCount * M * N * sizeof(float);
-  HK_RETURN_IF_ERROR(hk::device_workspace(part_bytes, &ws));
+  HK_RETURN_IF_ERROR(hk::device_workspace(part_bytes, stream, &ws));
   float* part = static_cast<float*>(ws);
   dim3 grid(static_cast<unsigned>(tiles), 1, batchCount * used);
   HK_RETURN_IF_ERROR(dispatch_layout<true>(ta, tb, grid, stream, M, N, K, alpha, A, lda, strideA,

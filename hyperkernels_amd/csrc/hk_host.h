@@ -22,13 +22,13 @@ namespace hk {
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
-// Device scratch owned by the library: one grow-only buffer per device, kept until the
-// process ends. The returned pointer is valid until the next call on the same device asks for
-// more bytes, so a launcher must fetch it once per call. Calls on one device that overlap in
-// time on different streams must not share it; the launchers here synchronise on nothing, so
-// the workspace is only handed to work on the caller's stream, and growing it waits for the
-// device first.
-hipError_t device_workspace(size_t bytes, void** out);
+// Scratch device memory for the launchers' multi-workgroup partials (split-K, reduce, the
+// LayerNorm gamma/beta partials): one grow-only buffer per (device, stream), held until the
+// process ends. Work on one stream runs in order, so consecutive calls on that stream reuse
+// the buffer safely; calls on different streams get different buffers. The pointer is valid
+// until the next call on the same (device, stream) asks for more bytes, so a launcher fetches
+// it once per call; growing it first waits for the work queued on that stream.
+hipError_t device_workspace(size_t bytes, hipStream_t stream, void** out);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }

@@ -381,7 +381,7 @@ hipError_t launch_bwd(const float* dy, const float* x, const float* mean, const 
     if (do_gb) {
       void* ws = nullptr;
       HK_RETURN_IF_ERROR(
-          hk::device_workspace(static_cast<size_t>(grid) * 2 * cols * sizeof(float), &ws));
+          hk::device_workspace(static_cast<size_t>(grid) * 2 * cols * sizeof(float), stream, &ws));
       part = static_cast<float*>(ws);
     }
     const size_t lds = do_gb ? static_cast<size_t>(kWavesPerBlock) * 2 * cols * sizeof(float) : 0;

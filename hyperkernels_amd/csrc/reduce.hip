@@ -207,7 +207,7 @@ hipError_t reduce_inner(const float* src, float* dst, int64_t nout, int64_t len,
   float* out = dst;
   if (split > 1) {
     void* ws = nullptr;
-    HK_RETURN_IF_ERROR(hk::device_workspace(static_cast<size_t>(split * nout) * sizeof(float), &ws));
+    HK_RETURN_IF_ERROR(hk::device_workspace(static_cast<size_t>(split * nout) * sizeof(float), stream, &ws));
     out = static_cast<float*>(ws);
   }
   hipLaunchKernelGGL(reduce_inner_block, dim3(static_cast<unsigned>(nout), static_cast<unsigned>(split)),
@@ -232,7 +232,7 @@ hipError_t reduce_outer_launch(const float* src, float* dst, int64_t nout, int64
   float* out = dst;
   if (split > 1) {
     void* ws = nullptr;
-    HK_RETURN_IF_ERROR(hk::device_workspace(static_cast<size_t>(split * nout) * sizeof(float), &ws));
+    HK_RETURN_IF_ERROR(hk::device_workspace(static_cast<size_t>(split * nout) * sizeof(float), stream, &ws));
     out = static_cast<float*>(ws);
   }
   hipLaunchKernelGGL(reduce_outer, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(split)),

@@ -1,5 +1,7 @@
-// runtime.hip - library-level state: ABI version, per-device facts and the device workspace.
+// runtime.hip - library-level state: ABI version, per-device facts and the workspaces.
+#include <map>
 #include <mutex>
+#include <utility>
 #include <vector>
 
 #include "hk_host.h"
@@ -13,11 +15,17 @@ namespace hk {
 namespace {
 struct DeviceState {
   int cu_count = 0;
-  void* ws = nullptr;
-  size_t ws_bytes = 0;
+};
+struct Workspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
 };
 std::mutex g_mu;
 std::vector<DeviceState> g_devices;
+// One grow-only workspace per (device, stream): work on one stream is ordered, so a call may
+// reuse the buffer the previous call on that stream used; calls on different streams never
+// share one.
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
 DeviceState* state_for_current(hipError_t* err) {
   int dev = 0;
@@ -45,24 +53,24 @@ int device_cu_count() {
   return s->cu_count;
 }
 
-hipError_t device_workspace(size_t bytes, void** out) {
+hipError_t device_workspace(size_t bytes, hipStream_t stream, void** out) {
   std::lock_guard<std::mutex> lk(g_mu);
-  hipError_t e;
-  DeviceState* s = state_for_current(&e);
-  if (!s) return e;
-  if (bytes > s->ws_bytes) {
-    if (s->ws) {
-      // Work already queued may still read the old buffer.
-      HK_RETURN_IF_ERROR(hipDeviceSynchronize());
-      HK_RETURN_IF_ERROR(hipFree(s->ws));
-      s->ws = nullptr;
-      s->ws_bytes = 0;
+  int dev = 0;
+  HK_RETURN_IF_ERROR(hipGetDevice(&dev));
+  Workspace& w = g_ws[std::make_pair(dev, stream)];
+  if (bytes > w.bytes) {
+    if (w.ptr) {
+      // Work already queued on this stream may still read the old buffer.
+      HK_RETURN_IF_ERROR(hipStreamSynchronize(stream));
+      HK_RETURN_IF_ERROR(hipFree(w.ptr));
+      w.ptr = nullptr;
+      w.bytes = 0;
     }
     size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
-    HK_RETURN_IF_ERROR(hipMalloc(&s->ws, want));
-    s->ws_bytes = want;
+    HK_RETURN_IF_ERROR(hipMalloc(&w.ptr, want));
+    w.bytes = want;
   }
-  *out = s->ws;
+  *out = w.ptr;
   return hipSuccess;
 }
 

@@ -461,7 +461,7 @@ hipError_t sgemm_run(bool ta, bool tb, int M, int N, int K, float alpha, const f
   const int used = static_cast<int>(hk::ceil_div(K, kps));
   void* ws = nullptr;
   HK_RETURN_IF_ERROR(hk::device_workspace(
-      static_cast<size_t>(used) * batchCount * M * N * sizeof(float), &ws));
+      static_cast<size_t>(used) * batchCount * M * N * sizeof(float), stream, &ws));
   float* part = static_cast<float*>(ws);
   dim3 grid(static_cast<unsigned>(tiles), 1, batchCount * used);
   HK_RETURN_IF_ERROR(dispatch_layout<true>(ta, tb, grid, stream, M, N, K, A, lda, strideA, B, ldb,

@@ -290,3 +290,27 @@ def test_sgemm_baseline_shape_split_k4_sampled_rows(hk, orc, lay):
     rel = max_rel(out[rows], ref)
     print(f"sgemm baseline rel {rel:.2e}")
     assert rel <= 2e-3
+
+
+def test_bgemm_split_k_on_concurrent_streams(hk, orc):
+    # Split-K partials live in a library workspace; two streams running split-K GEMMs at the
+    # same time must each get their own (a shared one would mix the partials).
+    lib = hk.lib()
+    say("bgemm split-K on two streams")
+    M, N, K = 512, 512, 2048
+    cases = []
+    for seed in (900, 910):
+        A, B, C0 = _operands(orc, M, N, K, 0, 0, seed)
+        cases.append((A, B, C0, to_dev_bf16(A), to_dev_bf16(B), to_dev_bf16(C0)))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for (A, B, C0, dA, dB, dC), s in zip(cases, streams):
+            with torch.cuda.stream(s):
+                st = lib.hk_bgemm_core(2, 4, M, N, K, bits(1.0), dA.data_ptr(), K, 0,
+                                       dB.data_ptr(), N, 0, bits(0.0), dC.data_ptr(), N, 0, 1,
+                                       s.cuda_stream)
+                assert st == 0
+        torch.cuda.synchronize()
+        for (A, B, C0, dA, dB, dC) in cases:
+            _check(orc, to_host_bits(dC), A, B, C0, 0, 0, 1.0, 0.0)
