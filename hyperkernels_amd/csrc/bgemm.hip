@@ -149,6 +149,21 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
   tn = in_group / gsz;
 }
 
+// Output transform: C = alpha * acc + beta * C, or, with a bias (bias != NULL),
+// C = alpha * acc + beta * bias and C is written without being read. The bias element of
+// output (row, col) is bias[row * brow + col * bcol]: (brow, bcol) = (0, 1) for a per-column
+// bias (numel N), (1, 0) per row (numel M), (0, 0) scalar (numel 1), (N, 1) full (numel M*N,
+// the same for every batch).
+struct Epi {
+  float alpha, beta;
+  const uint16_t* bias;
+  int64_t brow, bcol;
+};
+
+__device__ __forceinline__ float bias_at(const Epi& ep, int row, int col) {
+  return hk::bf16_to_f32(ep.bias[row * ep.brow + col * ep.bcol]);
+}
+
 // Scheduling hint: NR LDS reads spread over NM MFMAs (reads first in each pair), so the
 // operands of the next k step are fetched while the current one multiplies.
 template <int NM, int NR, int Q = 0>
@@ -163,6 +178,44 @@ __device__ __forceinline__ void interleave_reads() {
   }
 }
 
+// Writes the 4 x 4 accumulator blocks of a wave: for block (i, j) and quad q, output row
+// row0 + 32 i and columns col0 + 32 j + 8 q .. +3 (one 8-byte store).
+template <bool BIAS>
+__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[4][4], const Epi& ep,
+                                           uint16_t* Cb, int64_t ldc, int M, int N, int row0,
+                                           int col0) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + 32 * i;
+    if (row >= M) continue;
+    uint16_t* crow = Cb + static_cast<int64_t>(row) * ldc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int col = col0 + 32 * j + 8 * q;
+        if (col >= N) continue;
+        f32x2_t lo = f32x2_t{acc[i][j][4 * q], acc[i][j][4 * q + 1]} * ep.alpha;
+        f32x2_t hi = f32x2_t{acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]} * ep.alpha;
+        uint2* dst = reinterpret_cast<uint2*>(crow + col);
+        if (BIAS) {
+          lo += ep.beta * f32x2_t{bias_at(ep, row, col), bias_at(ep, row, col + 1)};
+          hi += ep.beta * f32x2_t{bias_at(ep, row, col + 2), bias_at(ep, row, col + 3)};
+        } else if (ep.beta != 0.0f) {
+          const uint2 old = *dst;
+          lo += ep.beta * f32x2_t{__uint_as_float(old.x << 16), __uint_as_float(old.x & 0xffff0000u)};
+          hi += ep.beta * f32x2_t{__uint_as_float(old.y << 16), __uint_as_float(old.y & 0xffff0000u)};
+        }
+        const bf16x2_t blo = __builtin_convertvector(lo, bf16x2_t);
+        const bf16x2_t bhi = __builtin_convertvector(hi, bf16x2_t);
+        uint2 v;
+        __builtin_memcpy(&v.x, &blo, 4);
+        __builtin_memcpy(&v.y, &bhi, 4);
+        *dst = v;
+      }
+  }
+}
+
 // Main loop per k-tile kt (ring slot kt % 2), 4 k steps of 16 MFMAs each:
 //   steps 0-2: operands of step s+1 are read from LDS between the MFMAs of step s;
 //   step 3:    wait for this wave's copies of tile kt+1, barrier (tile kt+1 visible to all,
@@ -173,8 +226,8 @@ __device__ __forceinline__ void interleave_reads() {
 // writes 8 bytes per quad straight from registers.
 template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL>
 __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
-    int M, int N, int K, float alpha, const uint16_t* __restrict__ A, int64_t lda, int64_t sA,
-    const uint16_t* __restrict__ B, int64_t ldb, int64_t sB, float beta, uint16_t* __restrict__ C,
+    int M, int N, int K, Epi ep, const uint16_t* __restrict__ A, int64_t lda, int64_t sA,
+    const uint16_t* __restrict__ B, int64_t ldb, int64_t sB, uint16_t* __restrict__ C,
     int64_t ldc, int64_t sC, int split_k, int k_per_split, float* __restrict__ part) {
   using OA = TileOperand<A_KMAJOR>;
   using OB = TileOperand<B_KMAJOR>;
@@ -344,40 +397,16 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
     return;
   }
   uint16_t* Cb = C + static_cast<int64_t>(batch) * sC;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = row0 + 32 * i;
-    if (row >= M) continue;
-    uint16_t* crow = Cb + static_cast<int64_t>(row) * ldc;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int col = col0 + 32 * j + 8 * q;
-        if (col >= N) continue;
-        f32x2_t lo = f32x2_t{acc[i][j][4 * q], acc[i][j][4 * q + 1]} * alpha;
-        f32x2_t hi = f32x2_t{acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]} * alpha;
-        uint2* dst = reinterpret_cast<uint2*>(crow + col);
-        if (beta != 0.0f) {
-          const uint2 old = *dst;
-          lo += beta * f32x2_t{__uint_as_float(old.x << 16), __uint_as_float(old.x & 0xffff0000u)};
-          hi += beta * f32x2_t{__uint_as_float(old.y << 16), __uint_as_float(old.y & 0xffff0000u)};
-        }
-        const bf16x2_t blo = __builtin_convertvector(lo, bf16x2_t);
-        const bf16x2_t bhi = __builtin_convertvector(hi, bf16x2_t);
-        uint2 v;
-        __builtin_memcpy(&v.x, &blo, 4);
-        __builtin_memcpy(&v.y, &bhi, 4);
-        *dst = v;
-      }
-  }
+  if (ep.bias)
+    store_tile<true>(acc, ep, Cb, ldc, M, N, row0, col0);
+  else
+    store_tile<false>(acc, ep, Cb, ldc, M, N, row0, col0);
 }
 
 // C = alpha * sum_s part[s] + beta * C (split order), fp32 -> bf16.
 __global__ __launch_bounds__(256) void bgemm_splitk_finalize(const float* __restrict__ part,
                                                              int split_k, int batch, int M, int N,
-                                                             float alpha, float beta,
-                                                             uint16_t* __restrict__ C,
+                                                             Epi ep, uint16_t* __restrict__ C,
                                                              int64_t ldc, int64_t sC) {
   // 4 consecutive outputs per thread (N is a multiple of 8 on the tiled path)
   const int64_t idx = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
@@ -392,10 +421,14 @@ __global__ __launch_bounds__(256) void bgemm_splitk_finalize(const float* __rest
     lo += f32x2_t{v.x, v.y};
     hi += f32x2_t{v.z, v.w};
   }
-  lo *= alpha;
-  hi *= alpha;
+  lo *= ep.alpha;
+  hi *= ep.alpha;
   uint2* dst = reinterpret_cast<uint2*>(C + b * sC + static_cast<int64_t>(row) * ldc + col);
-  if (beta != 0.0f) {
+  if (ep.bias) {
+    lo += ep.beta * f32x2_t{bias_at(ep, row, col), bias_at(ep, row, col + 1)};
+    hi += ep.beta * f32x2_t{bias_at(ep, row, col + 2), bias_at(ep, row, col + 3)};
+  } else if (ep.beta != 0.0f) {
+    const float beta = ep.beta;
     const uint2 old = *dst;
     lo += beta * f32x2_t{__uint_as_float(old.x << 16), __uint_as_float(old.x & 0xffff0000u)};
     hi += beta * f32x2_t{__uint_as_float(old.y << 16), __uint_as_float(old.y & 0xffff0000u)};
@@ -409,13 +442,12 @@ __global__ __launch_bounds__(256) void bgemm_splitk_finalize(const float* __rest
 }
 
 // Fallback: one thread per output, fp32 accumulation in k order.
-__global__ __launch_bounds__(256) void bgemm_simple(int ta, int tb, int M, int N, int K,
-                                                    float alpha, const uint16_t* __restrict__ A,
+__global__ __launch_bounds__(256) void bgemm_simple(int ta, int tb, int M, int N, int K, Epi ep,
+                                                    const uint16_t* __restrict__ A,
                                                     int64_t lda, int64_t sA,
                                                     const uint16_t* __restrict__ B, int64_t ldb,
-                                                    int64_t sB, float beta,
-                                                    uint16_t* __restrict__ C, int64_t ldc,
-                                                    int64_t sC) {
+                                                    int64_t sB, uint16_t* __restrict__ C,
+                                                    int64_t ldc, int64_t sC) {
   const int col = blockIdx.x * 16 + (threadIdx.x & 15);
   const int row = blockIdx.y * 16 + (threadIdx.x >> 4);
   const int b = blockIdx.z;
@@ -431,8 +463,9 @@ __global__ __launch_bounds__(256) void bgemm_simple(int ta, int tb, int M, int N
     acc += a * v;
   }
   uint16_t* dst = C + b * sC + static_cast<int64_t>(row) * ldc + col;
-  float f = alpha * acc;
-  if (beta != 0.0f) f += beta * hk::bf16_to_f32(*dst);
+  float f = ep.alpha * acc;
+  if (ep.bias) f += ep.beta * bias_at(ep, row, col);
+  else if (ep.beta != 0.0f) f += ep.beta * hk::bf16_to_f32(*dst);
   *dst = hk::f32_to_bf16(f);
 }
 
@@ -444,9 +477,9 @@ float bf16_bits_to_float(hk_bf16 h) {
 }
 
 template <bool AK, bool BKM, bool P>
-hipError_t launch_tiled(dim3 grid, hipStream_t stream, int M, int N, int K, float alpha,
+hipError_t launch_tiled(dim3 grid, hipStream_t stream, int M, int N, int K, const Epi& ep,
                         const uint16_t* A, int64_t lda, int64_t sA, const uint16_t* B,
-                        int64_t ldb, int64_t sB, float beta, uint16_t* C, int64_t ldc,
+                        int64_t ldb, int64_t sB, uint16_t* C, int64_t ldc,
                         int64_t sC, int split_k, int kps, float* part) {
   static std::once_flag once;
   static hipError_t attr_status = hipSuccess;
@@ -457,26 +490,26 @@ hipError_t launch_tiled(dim3 grid, hipStream_t stream, int M, int N, int K, floa
   });
   HK_RETURN_IF_ERROR(attr_status);
   hipLaunchKernelGGL((bgemm_tiled<AK, BKM, P>), grid, dim3(kThreads), kLdsBytes, stream, M, N, K,
-                     alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, split_k, kps, part);
+                     ep, A, lda, sA, B, ldb, sB, C, ldc, sC, split_k, kps, part);
   return hk::launch_status();
 }
 
 template <bool P>
 hipError_t dispatch_layout(bool ta, bool tb, dim3 grid, hipStream_t stream, int M, int N, int K,
-                           float alpha, const uint16_t* A, int64_t lda, int64_t sA,
-                           const uint16_t* B, int64_t ldb, int64_t sB, float beta, uint16_t* C,
+                           const Epi& ep, const uint16_t* A, int64_t lda, int64_t sA,
+                           const uint16_t* B, int64_t ldb, int64_t sB, uint16_t* C,
                            int64_t ldc, int64_t sC, int split_k, int kps, float* part) {
   // A is k-major unless transposed; B is k-major only when transposed.
   if (!ta && !tb)
-    return launch_tiled<true, false, P>(grid, stream, M, N, K, alpha, A, lda, sA, B, ldb, sB,
-                                        beta, C, ldc, sC, split_k, kps, part);
+    return launch_tiled<true, false, P>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
+                                        C, ldc, sC, split_k, kps, part);
   if (!ta && tb)
-    return launch_tiled<true, true, P>(grid, stream, M, N, K, alpha, A, lda, sA, B, ldb, sB,
-                                       beta, C, ldc, sC, split_k, kps, part);
+    return launch_tiled<true, true, P>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
+                                       C, ldc, sC, split_k, kps, part);
   if (ta && !tb)
-    return launch_tiled<false, false, P>(grid, stream, M, N, K, alpha, A, lda, sA, B, ldb, sB,
-                                         beta, C, ldc, sC, split_k, kps, part);
-  return launch_tiled<false, true, P>(grid, stream, M, N, K, alpha, A, lda, sA, B, ldb, sB, beta,
+    return launch_tiled<false, false, P>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
+                                         C, ldc, sC, split_k, kps, part);
+  return launch_tiled<false, true, P>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
                                       C, ldc, sC, split_k, kps, part);
 }
 
@@ -502,10 +535,14 @@ int auto_split_k(int64_t work_tiles, int64_t ktiles, int64_t outputs) {
   return best_s;
 }
 
+// bias == NULL: C = alpha * op(A) op(B) + beta * C. Otherwise C = alpha * op(A) op(B) +
+// beta * bias with bias_numel N (per column), M (per row), 1 (scalar) or M*N (full, shared by
+// all batches), tested in that order; C is then only written.
 hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_bits,
                      const hk_bf16* A, int lda, long long strideA, const hk_bf16* B, int ldb,
-                     long long strideB, hk_bf16 beta_bits, hk_bf16* C, int ldc, long long strideC,
-                     int batchCount, int splitK, hipStream_t stream) {
+                     long long strideB, hk_bf16 beta_bits, const hk_bf16* bias,
+                     int64_t bias_numel, hk_bf16* C, int ldc, long long strideC, int batchCount,
+                     int splitK, hipStream_t stream) {
   HK_CHECK_ARG(transA >= 0 && transA <= 2 && transB >= 0 && transB <= 2);
   // splitK == 0: the library picks the split (auto_split_k)
   HK_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batchCount >= 0 && splitK >= 0);
@@ -514,8 +551,14 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
   const bool ta = transA != 0, tb = transB != 0;  // OP_C is OP_T for real bf16
   HK_CHECK_ARG(K == 0 || (A != nullptr && B != nullptr));
   HK_CHECK_ARG(lda >= (ta ? M : K) && ldb >= (tb ? K : N));
-  const float alpha = bf16_bits_to_float(alpha_bits);
-  const float beta = bf16_bits_to_float(beta_bits);
+  Epi ep{bf16_bits_to_float(alpha_bits), bf16_bits_to_float(beta_bits), bias, 0, 0};
+  if (bias) {
+    if (bias_numel == N) ep.bcol = 1;
+    else if (bias_numel == M) ep.brow = 1;
+    else if (bias_numel == 1) { /* scalar: (0, 0) */ }
+    else if (bias_numel == static_cast<int64_t>(M) * N) { ep.brow = N; ep.bcol = 1; }
+    else return hipErrorInvalidValue;
+  }
 
   const int contig_a = ta ? M : K, contig_b = tb ? K : N;
   const bool tiled_ok = (contig_a % 8 == 0) && (contig_b % 8 == 0) && (N % 8 == 0) &&
@@ -528,8 +571,8 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
     if (K == 0) splitK = 1;
     dim3 grid((N + 15) / 16, (M + 15) / 16, batchCount);
     hipLaunchKernelGGL(bgemm_simple, grid, dim3(256), 0, stream, ta ? 1 : 0, tb ? 1 : 0, M, N,
-                       K, alpha, A, static_cast<int64_t>(lda), static_cast<int64_t>(strideA), B,
-                       static_cast<int64_t>(ldb), static_cast<int64_t>(strideB), beta, C,
+                       K, ep, A, static_cast<int64_t>(lda), static_cast<int64_t>(strideA), B,
+                       static_cast<int64_t>(ldb), static_cast<int64_t>(strideB), C,
                        static_cast<int64_t>(ldc), static_cast<int64_t>(strideC));
     return hk::launch_status();
   }
@@ -539,8 +582,8 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
   HK_CHECK_ARG(tiles <= INT32_MAX && static_cast<int64_t>(batchCount) * splitK <= 65535);
   if (splitK == 1) {
     dim3 grid(static_cast<unsigned>(tiles), 1, batchCount);
-    return dispatch_layout<false>(ta, tb, grid, stream, M, N, K, alpha, A, lda, strideA, B, ldb,
-                                  strideB, beta, C, ldc, strideC, 1, K, nullptr);
+    return dispatch_layout<false>(ta, tb, grid, stream, M, N, K, ep, A, lda, strideA, B, ldb,
+                                  strideB, C, ldc, strideC, 1, K, nullptr);
   }
   // k range per split rounded to the k-tile
   const int kps = static_cast<int>(hk::ceil_div(hk::ceil_div(K, splitK), BK) * BK);
@@ -550,12 +593,11 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
   HK_RETURN_IF_ERROR(hk::device_workspace(part_bytes, stream, &ws));
   float* part = static_cast<float*>(ws);
   dim3 grid(static_cast<unsigned>(tiles), 1, batchCount * used);
-  HK_RETURN_IF_ERROR(dispatch_layout<true>(ta, tb, grid, stream, M, N, K, alpha, A, lda, strideA,
-                                           B, ldb, strideB, beta, C, ldc, strideC, used, kps,
-                                           part));
+  HK_RETURN_IF_ERROR(dispatch_layout<true>(ta, tb, grid, stream, M, N, K, ep, A, lda, strideA,
+                                           B, ldb, strideB, C, ldc, strideC, used, kps, part));
   const int64_t total = static_cast<int64_t>(M) * N * batchCount;
   hipLaunchKernelGGL(bgemm_splitk_finalize, dim3(static_cast<unsigned>(hk::ceil_div(total, 1024))),
-                     dim3(256), 0, stream, part, used, batchCount, M, N, alpha, beta, C,
+                     dim3(256), 0, stream, part, used, batchCount, M, N, ep, C,
                      static_cast<int64_t>(ldc), static_cast<int64_t>(strideC));
   return hk::launch_status();
 }
@@ -566,8 +608,8 @@ extern "C" hipError_t hk_bgemm(int transA, int transB, int M, int N, int K, hk_b
                                const hk_bf16* A, int lda, long long strideA, const hk_bf16* B,
                                int ldb, long long strideB, hk_bf16 beta, hk_bf16* C, int ldc,
                                long long strideC, int batchCount, hipStream_t stream) {
-  return bgemm_run(transA, transB, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, C, ldc,
-                   strideC, batchCount, 0, stream);
+  return bgemm_run(transA, transB, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta,
+                   nullptr, 0, C, ldc, strideC, batchCount, 0, stream);
 }
 
 extern "C" hipError_t hk_bgemm_core(int layout, int splitK, int M, int N, int K, hk_bf16 alpha,
@@ -580,8 +622,8 @@ extern "C" hipError_t hk_bgemm_core(int layout, int splitK, int M, int N, int K,
   HK_CHECK_ARG(splitK >= 1);
   const int ta = layout == HK_LAYOUT_TN ? 1 : 0;
   const int tb = layout == HK_LAYOUT_NT ? 1 : 0;
-  return bgemm_run(ta, tb, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, C, ldc,
-                   strideC, batchCount, splitK, stream);
+  return bgemm_run(ta, tb, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, nullptr, 0,
+                   C, ldc, strideC, batchCount, splitK, stream);
 }
 
 extern "C" hipError_t hk_bgemm_nt_backward(int M, int N, int K, hk_bf16 alpha, const hk_bf16* A,
@@ -589,8 +631,8 @@ extern "C" hipError_t hk_bgemm_nt_backward(int M, int N, int K, hk_bf16 alpha, c
                                            long long strideB, hk_bf16 beta, hk_bf16* C, int ldc,
                                            long long strideC, int batchCount,
                                            hipStream_t stream) {
-  return bgemm_run(0, 1, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, C, ldc, strideC,
-                   batchCount, 0, stream);
+  return bgemm_run(0, 1, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, nullptr, 0,
+                   C, ldc, strideC, batchCount, 0, stream);
 }
 
 extern "C" hipError_t hk_bgemm_tn_backward(int M, int N, int K, hk_bf16 alpha, const hk_bf16* A,
@@ -598,6 +640,31 @@ extern "C" hipError_t hk_bgemm_tn_backward(int M, int N, int K, hk_bf16 alpha, c
                                            long long strideB, hk_bf16 beta, hk_bf16* C, int ldc,
                                            long long strideC, int batchCount,
                                            hipStream_t stream) {
-  return bgemm_run(1, 0, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, C, ldc, strideC,
-                   batchCount, 0, stream);
+  return bgemm_run(1, 0, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, nullptr, 0,
+                   C, ldc, strideC, batchCount, 0, stream);
+}
+
+extern "C" hipError_t hk_bgemm_addmm(int M, int N, int K, hk_bf16 alpha, const hk_bf16* A, int lda,
+                                     long long strideA, const hk_bf16* B, int ldb,
+                                     long long strideB, hk_bf16 beta, const hk_bf16* bias,
+                                     int64_t bias_numel, hk_bf16* C, int ldc, long long strideC,
+                                     int batchCount, hipStream_t stream) {
+  // C is only written: without a bias the product is C = alpha * A B (bgemm_addmm…:214-300)
+  if (!bias) beta = 0;
+  return bgemm_run(0, 0, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, bias,
+                   bias_numel, C, ldc, strideC, batchCount, 0, stream);
+}
+
+extern "C" hipError_t hk_bgemm_core_bias(int layout, int splitK, int M, int N, int K, hk_bf16 alpha,
+                                         const hk_bf16* A, int lda, long long strideA,
+                                         const hk_bf16* B, int ldb, long long strideB,
+                                         hk_bf16 beta, const hk_bf16* bias, int64_t bias_numel,
+                                         hk_bf16* C, int ldc, long long strideC, int batchCount,
+                                         hipStream_t stream) {
+  HK_CHECK_ARG(layout >= HK_LAYOUT_NT && layout <= HK_LAYOUT_NN);
+  HK_CHECK_ARG(splitK >= 1);
+  const int ta = layout == HK_LAYOUT_TN ? 1 : 0;
+  const int tb = layout == HK_LAYOUT_NT ? 1 : 0;
+  return bgemm_run(ta, tb, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, bias,
+                   bias_numel, C, ldc, strideC, batchCount, splitK, stream);
 }

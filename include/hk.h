@@ -231,6 +231,32 @@ HK_API hipError_t hk_bgemm_tn_backward(int M, int N, int K, hk_bf16 alpha, const
                                        long long strideB, hk_bf16 beta, hk_bf16* C, int ldc,
                                        long long strideC, int batchCount, hipStream_t stream);
 
+/* BF16 GEMM with a bias, one semantics for both entry points:
+ *   C = alpha * op(A) op(B) + beta * bias, C written and not read, the bias element of output
+ *   (row, col) chosen by bias_numel: N -> bias[col], else M -> bias[row], else 1 -> bias[0],
+ *   else M*N -> bias[row * N + col] (one M x N bias for every batch); any other bias_numel is
+ *   rejected.
+ * hk_bgemm_addmm replaces bgemm_addmm_kernel<BM, BN, BK, STAGES, THREADS, Aligned>
+ *   (blas/bf16/bgemm_addmm_sm89_kernel.cu:15-24; epilogue :214-300), NN only, and keeps its
+ *   argument order. bias == NULL gives C = alpha * A B (the kernel adds beta * 0 then); the
+ *   reference's kernel accepts bias_numel 1, N and M*N, and its test computes
+ *   alpha * A B + beta * bias (test_bgemm_addmm_sm89.cu:50-53, 91-94), which is what this
+ *   entry point computes.
+ * hk_bgemm_core_bias is hk_bgemm_core with the split-K bias initialisation of
+ *   bgemm_scale_template_kernel (blas/bf16/bgemm_core_template.cu:270-289: C <- beta * bias,
+ *   bias_numel N, M, 1 or M*N, before the splits accumulate): bias == NULL gives
+ *   hk_bgemm_core's C = alpha * op(A) op(B) + beta * C. */
+HK_API hipError_t hk_bgemm_addmm(int M, int N, int K, hk_bf16 alpha, const hk_bf16* A, int lda,
+                                 long long strideA, const hk_bf16* B, int ldb, long long strideB,
+                                 hk_bf16 beta, const hk_bf16* bias, int64_t bias_numel,
+                                 hk_bf16* C, int ldc, long long strideC, int batchCount,
+                                 hipStream_t stream);
+HK_API hipError_t hk_bgemm_core_bias(int layout, int splitK, int M, int N, int K, hk_bf16 alpha,
+                                     const hk_bf16* A, int lda, long long strideA,
+                                     const hk_bf16* B, int ldb, long long strideB, hk_bf16 beta,
+                                     const hk_bf16* bias, int64_t bias_numel, hk_bf16* C, int ldc,
+                                     long long strideC, int batchCount, hipStream_t stream);
+
 /* ------------------------------------------------------------------------------------------
  * FP32 batched GEMM on fp32 MFMA (full fp32 products; the reference uses single-pass TF32),
  * row-major, layout HK_LAYOUT_{NT,TN,NN} as SgemmLayout (blas/fp32/sgemm_sm89_core_template.cu:9).

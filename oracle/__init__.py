@@ -75,7 +75,7 @@ _SIGS = {
     "oracle_sgemm": (None, [_i, _i, _i64, _i64, _i64, _f, _f32p, _i64, _f32p, _i64, _f,
                             _NullableF32, _i64, _NullableF32, _f32p, _i64]),
     "oracle_bgemm": (None, [_i, _i, _i64, _i64, _i64, _f, _u16p, _i64, _u16p, _i64, _f,
-                            _NullableU16, _i64, _NullableU16, _f32p, _i64]),
+                            _NullableU16, _i64, _NullableU16, _i64, _f32p, _i64]),
 }
 
 _lib = None
@@ -302,7 +302,8 @@ def sgemm(transA, transB, A, B, alpha=1.0, beta=0.0, C0=None, bias=None):
 
 
 def bgemm(transA, transB, A, B, alpha=1.0, beta=0.0, C0=None, bias=None):
-    """bf16 (uint16) operands, fp32 result = alpha acc + beta C0 (+ beta bias)."""
+    """bf16 (uint16) operands, fp32 result = alpha acc + beta C0 (+ beta bias). The bias
+    element is chosen by its size: N per column, M per row, 1 scalar, M*N full."""
     A, B = _c(A, np.uint16), _c(B, np.uint16)
     M = A.shape[1] if transA else A.shape[0]
     K = A.shape[0] if transA else A.shape[1]
@@ -310,5 +311,6 @@ def bgemm(transA, transB, A, B, alpha=1.0, beta=0.0, C0=None, bias=None):
     C = np.empty((M, N), np.float32)
     lib().oracle_bgemm(int(transA), int(transB), M, N, K, alpha, A, A.shape[1], B, B.shape[1], beta,
                        None if C0 is None else _c(C0, np.uint16), N,
-                       None if bias is None else _c(bias, np.uint16), C, N)
+                       None if bias is None else _c(bias, np.uint16).reshape(-1),
+                       0 if bias is None else int(np.asarray(bias).size), C, N)
     return C

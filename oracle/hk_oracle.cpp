@@ -427,7 +427,10 @@ ORACLE_API void oracle_sgemm(int transA, int transB, int64_t M, int64_t N, int64
 ORACLE_API void oracle_bgemm(int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha,
                              const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb,
                              float beta, const uint16_t* C0, int64_t ldc0, const uint16_t* bias,
-                             float* C, int64_t ldc) {
+                             int64_t bias_numel, float* C, int64_t ldc) {
+  // bias (bgemm_addmm_sm89_kernel.cu:214-300; bgemm_core_template.cu:270-289): element
+  // (r, c) uses bias[c] when bias_numel == N, else bias[r] when == M, else bias[0] when == 1,
+  // else bias[r * N + c] (M * N); the result adds beta * bias.
 #pragma omp parallel for schedule(static)
   for (int64_t r = 0; r < M; ++r) {
     for (int64_t c = 0; c < N; ++c) {
@@ -438,7 +441,11 @@ ORACLE_API void oracle_bgemm(int transA, int transB, int64_t M, int64_t N, int64
         acc += a * b;
       }
       float out = alpha * acc + (C0 ? beta * bf16_to_f32(C0[r * ldc0 + c]) : 0.0f);
-      if (bias) out += beta * bf16_to_f32(bias[c]);
+      if (bias) {
+        const int64_t i =
+            bias_numel == N ? c : bias_numel == M ? r : bias_numel == 1 ? 0 : r * N + c;
+        out += beta * bf16_to_f32(bias[i]);
+      }
       C[r * ldc + c] = out;
     }
   }

@@ -314,3 +314,57 @@ def test_bgemm_split_k_on_concurrent_streams(hk, orc):
         torch.cuda.synchronize()
         for (A, B, C0, dA, dB, dC) in cases:
             _check(orc, to_host_bits(dC), A, B, C0, 0, 0, 1.0, 0.0)
+
+
+@pytest.mark.parametrize("numel", ["N", "M", "1", "MN", "none"])
+@pytest.mark.parametrize("M,N,K", [(256, 512, 128), (300, 264, 136), (17, 9, 33)])
+def test_bgemm_addmm_bias_forms(hk, orc, numel, M, N, K):
+    # bgemm_addmm_kernel: C = alpha A B + beta bias, C not read (test_bgemm_addmm_sm89.cu:91-94)
+    say("bgemm addmm", numel, M, N, K)
+    lib = hk.lib()
+    A, B, C0 = _operands(orc, M, N, K, 0, 0, 700)
+    size = {"N": N, "M": M, "1": 1, "MN": M * N, "none": 0}[numel]
+    bias = orc.f32_to_bf16(orc.splitmix_uniform(max(size, 1), 701)) if size else None
+    dA, dB, dC = to_dev_bf16(A), to_dev_bf16(B), to_dev_bf16(C0)
+    dbias = to_dev_bf16(bias) if size else None
+    st = lib.hk_bgemm_addmm(M, N, K, bits(1.5), dA.data_ptr(), K, 0, dB.data_ptr(), N, 0,
+                            bits(0.5), dbias.data_ptr() if size else None, size, dC.data_ptr(),
+                            N, 0, 1, torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    out = to_host_bits(dC)
+    # C is only written: the previous contents (C0) must not contribute
+    ref = (orc.bgemm(0, 0, A, B, alpha=1.5, beta=0.5, bias=bias) if size
+           else orc.bgemm(0, 0, A, B, alpha=1.5))
+    assert max_rel(orc.bf16_to_f32(out), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("split_k", [1, 3])
+def test_bgemm_core_bias_split_k(hk, orc, ta, tb, split_k):
+    # core template with the split-K bias initialisation (bgemm_core_template.cu:270-289)
+    M, N, K = 264, 520, 328
+    say("bgemm core bias", ta, tb, split_k)
+    lib = hk.lib()
+    A, B, C0 = _operands(orc, M, N, K, ta, tb, 720)
+    bias = orc.f32_to_bf16(orc.splitmix_uniform(M, 721))  # per-row form
+    dA, dB, dC = to_dev_bf16(A), to_dev_bf16(B), to_dev_bf16(C0)
+    dbias = to_dev_bf16(bias)
+    layout = {(0, 1): 0, (1, 0): 1, (0, 0): 2}[(ta, tb)]
+    st = lib.hk_bgemm_core_bias(layout, split_k, M, N, K, bits(1.0), dA.data_ptr(), A.shape[1], 0,
+                                dB.data_ptr(), B.shape[1], 0, bits(2.0), dbias.data_ptr(), M,
+                                dC.data_ptr(), N, 0, 1, torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    ref = orc.bgemm(ta, tb, A, B, alpha=1.0, beta=2.0, bias=bias)
+    assert max_rel(orc.bf16_to_f32(to_host_bits(dC)), ref) <= 1e-2
+
+
+def test_bgemm_addmm_rejects_unknown_bias_size(hk, orc):
+    lib = hk.lib()
+    M, N, K = 64, 64, 64
+    A, B, C0 = _operands(orc, M, N, K, 0, 0, 730)
+    dA, dB, dC = to_dev_bf16(A), to_dev_bf16(B), to_dev_bf16(C0)
+    dbias = to_dev_bf16(orc.f32_to_bf16(orc.splitmix_uniform(7, 731)))
+    st = lib.hk_bgemm_addmm(M, N, K, bits(1.0), dA.data_ptr(), K, 0, dB.data_ptr(), N, 0,
+                            bits(1.0), dbias.data_ptr(), 7, dC.data_ptr(), N, 0, 1,
+                            torch.cuda.current_stream().cuda_stream)
+    assert st == 1  # hipErrorInvalidValue

@@ -308,3 +308,19 @@ def test_bgemm_vs_numpy(orc, ta, tb):
     b = orc.bf16_to_f32(B).astype(np.float64)
     ref = (a.T if ta else a) @ (b.T if tb else b) + 0.5 * orc.bf16_to_f32(C0)
     assert max_rel(got, ref) < 1e-5
+
+
+@pytest.mark.parametrize("numel", ["N", "M", "1", "MN"])
+def test_bgemm_bias_forms_vs_numpy(orc, numel):
+    # addmm / split-K bias init forms (bgemm_addmm…:246-300, bgemm_core_template.cu:277-283)
+    M, N, K = 24, 40, 56
+    A = orc.f32_to_bf16(orc.splitmix_uniform(M * K, 15)).reshape(M, K)
+    B = orc.f32_to_bf16(orc.splitmix_uniform(K * N, 16)).reshape(K, N)
+    size = {"N": N, "M": M, "1": 1, "MN": M * N}[numel]
+    bias = orc.f32_to_bf16(orc.splitmix_uniform(size, 17))
+    got = orc.bgemm(0, 0, A, B, alpha=1.5, beta=0.5, bias=bias)
+    b64 = orc.bf16_to_f32(bias).astype(np.float64)
+    bfull = {"N": lambda: b64[None, :], "M": lambda: b64[:, None],
+             "1": lambda: b64.reshape(1, 1), "MN": lambda: b64.reshape(M, N)}[numel]()
+    ref = 1.5 * (orc.bf16_to_f32(A).astype(np.float64) @ orc.bf16_to_f32(B)) + 0.5 * bfull
+    assert max_rel(got, np.broadcast_to(ref, (M, N))) < 1e-5
