@@ -225,6 +225,25 @@ def per_kernel_suite(flush):
         ("ln_bwd_fused", lambda: hk.layer_norm_backward(dy, x, mean, rstd, gamma, dgam, dbet, dx),
          W.ln_bwd_bytes(R, C), "hbm"),
     ]
+    # the same LayerNorm in bf16 and fp16 storage (fp32 statistics)
+    for dt, tag in ((torch.bfloat16, "bf16"), (torch.float16, "f16")):
+        x16, g16, b16, dy16 = x.to(dt), gamma.to(dt), beta.to(dt), dy.to(dt)
+        y16, dx16 = torch.empty_like(x16), torch.empty_like(x16)
+        cases += [
+            (f"ln_fwd_{tag}", lambda x16=x16, g16=g16, b16=b16, y16=y16: hk.layer_norm_forward(
+                x16, g16, b16, W.LN["eps"], y16, mean, rstd), W.ln_fwd_bytes(R, C, 2), "hbm"),
+            (f"ln_bwd_fused_{tag}", lambda dy16=dy16, x16=x16, g16=g16, dx16=dx16:
+                hk.layer_norm_backward(dy16, x16, mean, rstd, g16, dgam, dbet, dx16),
+             W.ln_bwd_bytes(R, C, 2), "hbm"),
+        ]
+    # GELU in fp16 at the configs[1] shape (the headline step runs the bf16 form)
+    n = W.numel(W.GELU["shape"])
+    gx = torch.randn(n, generator=g, device=DEV).half()
+    gg = torch.randn(n, generator=g, device=DEV).half()
+    gy, gi = torch.empty_like(gx), torch.empty_like(gx)
+    cases += [("gelu_fwd_f16", lambda: hk.gelu_forward(gx, gy), W.gelu_fwd_bytes(n, 2), "hbm"),
+              ("gelu_bwd_f16", lambda: hk.gelu_backward(gg, gx, gi), W.gelu_bwd_bytes(n, 2),
+               "hbm")]
     # unified reduce at the README shape
     rs = torch.randn(16384, 50304, generator=g, device=DEV)
     lay = hk.ReductionLayout()

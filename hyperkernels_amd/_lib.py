@@ -28,6 +28,7 @@ _C_TYPES = {
     "long long": ctypes.c_longlong,
     "float": ctypes.c_float,
     "hk_bf16": ctypes.c_uint16,
+    "hk_f16": ctypes.c_uint16,
     "hipError_t": ctypes.c_int,
     "hipStream_t": ctypes.c_void_p,
     "size_t": ctypes.c_size_t,

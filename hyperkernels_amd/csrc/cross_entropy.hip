@@ -6,6 +6,9 @@
 //             loss = log(sum) + max - x[target]; saves max and sum for the backward.
 //   backward  kernels/loss/sparseCENormalize_from_stats.cu:7-49
 //             grad_j = (exp(x_j - max) / sum - [j == target]) * (*grad_output * host_scale)
+//   target index types int32, int64 and uint16, as the reference instantiates both kernels
+//             (sparse_ce_forward_kernel_vec_save_stats.cu:108-113;
+//             sparseCENormalize_from_stats.cu:52-60). The index is widened to int64 before use.
 //
 // Design (gfx950): one 1024-lane workgroup streams one row in the forward. A row of fp32 logits starts at
 // row * vocab * 4 bytes, which is only 4-byte aligned when vocab is odd (the GPT-2 vocabulary
@@ -54,8 +57,9 @@ constexpr int kFwdThreads = 1024;
 constexpr int kFwdWaves = kFwdThreads / HK_WAVE;
 constexpr int kFwdUnroll = 2;
 
+template <typename TIdx>
 __global__ __launch_bounds__(kFwdThreads) void ce_forward(const float* __restrict__ logits,
-                                                          const int32_t* __restrict__ targets,
+                                                          const TIdx* __restrict__ targets,
                                                           float* __restrict__ losses,
                                                           float* __restrict__ saved_max,
                                                           float* __restrict__ saved_sum,
@@ -125,8 +129,9 @@ __device__ __forceinline__ float ce_grad1(float v, float mx, float inv_sum, floa
 constexpr int kBwdThreads = 512;
 constexpr int kChunkVec = kBwdThreads;
 
+template <typename TIdx>
 __global__ __launch_bounds__(kBwdThreads) void ce_backward(
-    const float* __restrict__ logits, const int32_t* __restrict__ targets,
+    const float* __restrict__ logits, const TIdx* __restrict__ targets,
     float* __restrict__ grad, const float* __restrict__ saved_max,
     const float* __restrict__ saved_sum, int64_t vocab, int nchunks,
     const float* __restrict__ grad_output, float host_scale) {
@@ -163,8 +168,9 @@ __global__ __launch_bounds__(kBwdThreads) void ce_backward(
 }
 
 // Scalar path for a grad buffer whose 16-byte phase differs from the logits buffer's.
+template <typename TIdx>
 __global__ __launch_bounds__(kThreads) void ce_backward_scalar(
-    const float* __restrict__ logits, const int32_t* __restrict__ targets,
+    const float* __restrict__ logits, const TIdx* __restrict__ targets,
     float* __restrict__ grad, const float* __restrict__ saved_max,
     const float* __restrict__ saved_sum, int64_t vocab, const float* __restrict__ grad_output,
     float host_scale) {
@@ -179,41 +185,60 @@ __global__ __launch_bounds__(kThreads) void ce_backward_scalar(
     g[j] = ce_grad1(x[j], mx, inv_sum, scale, j == t);
 }
 
-}  // namespace
-
-extern "C" hipError_t hk_sparse_ce_forward_f32_i32(const float* logits, const int32_t* targets,
-                                                   float* losses, float* saved_max,
-                                                   float* saved_sum, int64_t batch_size,
-                                                   int64_t vocab_size, hipStream_t stream) {
+template <typename TIdx>
+hipError_t ce_forward_launch(const float* logits, const TIdx* targets, float* losses,
+                             float* saved_max, float* saved_sum, int64_t batch_size,
+                             int64_t vocab_size, hipStream_t stream) {
   HK_CHECK_ARG(batch_size >= 0 && vocab_size >= 1 && batch_size <= INT32_MAX);
   if (batch_size == 0) return hipSuccess;
   HK_CHECK_ARG(logits && targets && losses && saved_max && saved_sum);
-  hipLaunchKernelGGL(ce_forward, dim3(static_cast<unsigned>(batch_size)), dim3(kFwdThreads), 0,
-                     stream, logits, targets, losses, saved_max, saved_sum, vocab_size);
+  hipLaunchKernelGGL(ce_forward<TIdx>, dim3(static_cast<unsigned>(batch_size)), dim3(kFwdThreads),
+                     0, stream, logits, targets, losses, saved_max, saved_sum, vocab_size);
   return hk::launch_status();
 }
 
-extern "C" hipError_t hk_sparse_ce_backward_f32_i32(const float* logits, const int32_t* targets,
-                                                    float* grad, const float* saved_max,
-                                                    const float* saved_sum, int64_t batch_size,
-                                                    int64_t vocab_size, const float* grad_output,
-                                                    float host_scale, hipStream_t stream) {
+template <typename TIdx>
+hipError_t ce_backward_launch(const float* logits, const TIdx* targets, float* grad,
+                              const float* saved_max, const float* saved_sum, int64_t batch_size,
+                              int64_t vocab_size, const float* grad_output, float host_scale,
+                              hipStream_t stream) {
   HK_CHECK_ARG(batch_size >= 0 && vocab_size >= 1 && batch_size <= INT32_MAX);
   if (batch_size == 0) return hipSuccess;
   HK_CHECK_ARG(logits && targets && grad && saved_max && saved_sum);
   const bool same_phase = ((reinterpret_cast<uintptr_t>(logits) ^
                             reinterpret_cast<uintptr_t>(grad)) & 15u) == 0;
   if (!same_phase) {
-    hipLaunchKernelGGL(ce_backward_scalar, dim3(static_cast<unsigned>(batch_size)), dim3(kThreads),
-                       0, stream, logits, targets, grad, saved_max, saved_sum, vocab_size,
-                       grad_output, host_scale);
+    hipLaunchKernelGGL(ce_backward_scalar<TIdx>, dim3(static_cast<unsigned>(batch_size)),
+                       dim3(kThreads), 0, stream, logits, targets, grad, saved_max, saved_sum,
+                       vocab_size, grad_output, host_scale);
     return hk::launch_status();
   }
   // body vectors per row are at most vocab / 4; at least one chunk per row (head/tail only)
   const int64_t nchunks = hk::ceil_div(vocab_size / 4 + 1, kChunkVec);
   HK_CHECK_ARG(nchunks <= INT32_MAX && batch_size * nchunks <= INT32_MAX);
-  hipLaunchKernelGGL(ce_backward, dim3(static_cast<unsigned>(batch_size * nchunks)),
+  hipLaunchKernelGGL(ce_backward<TIdx>, dim3(static_cast<unsigned>(batch_size * nchunks)),
                      dim3(kBwdThreads), 0, stream, logits, targets, grad, saved_max, saved_sum,
                      vocab_size, static_cast<int>(nchunks), grad_output, host_scale);
   return hk::launch_status();
 }
+
+}  // namespace
+
+#define HK_CE_ENTRY_POINTS(SUFFIX, TIdx)                                                          \
+  extern "C" hipError_t hk_sparse_ce_forward_f32_##SUFFIX(                                       \
+      const float* logits, const TIdx* targets, float* losses, float* saved_max,                 \
+      float* saved_sum, int64_t batch_size, int64_t vocab_size, hipStream_t stream) {            \
+    return ce_forward_launch<TIdx>(logits, targets, losses, saved_max, saved_sum, batch_size,    \
+                                   vocab_size, stream);                                          \
+  }                                                                                              \
+  extern "C" hipError_t hk_sparse_ce_backward_f32_##SUFFIX(                                      \
+      const float* logits, const TIdx* targets, float* grad, const float* saved_max,             \
+      const float* saved_sum, int64_t batch_size, int64_t vocab_size, const float* grad_output,  \
+      float host_scale, hipStream_t stream) {                                                    \
+    return ce_backward_launch<TIdx>(logits, targets, grad, saved_max, saved_sum, batch_size,     \
+                                    vocab_size, grad_output, host_scale, stream);                \
+  }
+
+HK_CE_ENTRY_POINTS(i32, int32_t)
+HK_CE_ENTRY_POINTS(i64, int64_t)
+HK_CE_ENTRY_POINTS(u16, uint16_t)

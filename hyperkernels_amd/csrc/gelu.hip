@@ -1,4 +1,4 @@
-// gelu.hip - tanh-approximation GELU forward/backward, fp32 math, fp32 or bf16 I/O.
+// gelu.hip - tanh-approximation GELU forward/backward, fp32 math, fp32, bf16 or fp16 I/O.
 //
 // Reference behaviour: kernels/gelu/gelu_forward_sm89_kernel.cu:19-22 (forward formula) and
 // kernels/gelu/gelu_backward_sm89_kernel.cu:24-30 (analytic derivative). The reference uses the
@@ -6,7 +6,10 @@
 // 1 + tanh(u) and 1 - tanh(u)^2, which are evaluated through the logistic function
 // (1 + tanh(u)) / 2 = 1 / (1 + exp(-2u)) with relative error of a few ulp everywhere.
 //
-// HBM layout: flat contiguous tensors. Each lane moves 16 bytes per access (8 bf16 or
+// The three storage types are the reference's instantiations (gelu_forward_sm89_kernel.cu:78-80;
+// gelu_backward_sm89_kernel.cu:88-90); 16-bit results are rounded to nearest even.
+//
+// HBM layout: flat contiguous tensors. Each lane moves 16 bytes per access (8 bf16 / fp16 or
 // 4 fp32) and a workgroup of 256 lanes covers kUnroll consecutive 4 KiB spans, so every wave
 // issues fully coalesced 1 KiB transactions. One span per workgroup (kUnroll = 1) measured
 // fastest on MI355X at the GPT-2 shape (25.2 M bf16: 22 us forward, 28.5 us backward, against
@@ -44,44 +47,11 @@ __device__ __forceinline__ float gelu_grad(float x) {
   return s + 2.0f * x * (s * (1.0f - s)) * du;
 }
 
-// Element access for the two storage types.
-template <typename T> struct Elem;
-template <> struct Elem<float> {
-  static constexpr int kPerVec = 4;
-  __device__ static float load(const float* p, int64_t i) { return p[i]; }
-  __device__ static void store(float* p, int64_t i, float v) { p[i] = v; }
-  __device__ static void unpack(const uint4& r, float* f) {
-    f[0] = __uint_as_float(r.x); f[1] = __uint_as_float(r.y);
-    f[2] = __uint_as_float(r.z); f[3] = __uint_as_float(r.w);
-  }
-  __device__ static uint4 pack(const float* f) {
-    return make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
-                      __float_as_uint(f[3]));
-  }
-};
-template <> struct Elem<uint16_t> {
-  static constexpr int kPerVec = 8;
-  __device__ static float load(const uint16_t* p, int64_t i) { return hk::bf16_to_f32(p[i]); }
-  __device__ static void store(uint16_t* p, int64_t i, float v) { p[i] = hk::f32_to_bf16(v); }
-  __device__ static void unpack(const uint4& r, float* f) {
-    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      f[2 * k] = __uint_as_float(w[k] << 16);
-      f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
-    }
-  }
-  __device__ static uint4 pack(const float* f) {
-    return make_uint4(hk::pack_bf16x2(f[0], f[1]), hk::pack_bf16x2(f[2], f[3]),
-                      hk::pack_bf16x2(f[4], f[5]), hk::pack_bf16x2(f[6], f[7]));
-  }
-};
-
 // Vector body: nvec 16-byte vectors, all pointers 16-byte aligned.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void gelu_fwd_vec(const uint4* __restrict__ in,
                                                          uint4* __restrict__ out, int64_t nvec) {
-  constexpr int P = Elem<T>::kPerVec;
+  constexpr int P = T::kPerVec;
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads * kUnroll + threadIdx.x;
   uint4 r[kUnroll];
 #pragma unroll
@@ -94,10 +64,10 @@ __global__ __launch_bounds__(kThreads) void gelu_fwd_vec(const uint4* __restrict
     const int64_t i = base + u * kThreads;
     if (i < nvec) {
       float f[P];
-      Elem<T>::unpack(r[u], f);
+      T::unpack(r[u], f);
 #pragma unroll
       for (int k = 0; k < P; ++k) f[k] = gelu_fwd(f[k]);
-      hk::st_nt(out + i, Elem<T>::pack(f));
+      hk::st_nt(out + i, T::pack(f));
     }
   }
 }
@@ -107,7 +77,7 @@ __global__ __launch_bounds__(kThreads) void gelu_bwd_vec(const uint4* __restrict
                                                          const uint4* __restrict__ in,
                                                          uint4* __restrict__ grad_in,
                                                          int64_t nvec) {
-  constexpr int P = Elem<T>::kPerVec;
+  constexpr int P = T::kPerVec;
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads * kUnroll + threadIdx.x;
   uint4 rg[kUnroll], rx[kUnroll];
 #pragma unroll
@@ -123,35 +93,35 @@ __global__ __launch_bounds__(kThreads) void gelu_bwd_vec(const uint4* __restrict
     const int64_t i = base + u * kThreads;
     if (i < nvec) {
       float g[P], x[P];
-      Elem<T>::unpack(rg[u], g);
-      Elem<T>::unpack(rx[u], x);
+      T::unpack(rg[u], g);
+      T::unpack(rx[u], x);
 #pragma unroll
       for (int k = 0; k < P; ++k) g[k] = g[k] * gelu_grad(x[k]);
-      hk::st_nt(grad_in + i, Elem<T>::pack(g));
+      hk::st_nt(grad_in + i, T::pack(g));
     }
   }
 }
 
 // Scalar path: tails and unaligned tensors.
-template <typename T>
-__global__ __launch_bounds__(kThreads) void gelu_fwd_scalar(const T* __restrict__ in,
-                                                            T* __restrict__ out, int64_t begin,
+template <typename T, typename S = typename T::storage>
+__global__ __launch_bounds__(kThreads) void gelu_fwd_scalar(const S* __restrict__ in,
+                                                            S* __restrict__ out, int64_t begin,
                                                             int64_t end) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
   for (int64_t i = begin + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < end;
        i += stride)
-    Elem<T>::store(out, i, gelu_fwd(Elem<T>::load(in, i)));
+    T::store(out, i, gelu_fwd(T::load(in, i)));
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) void gelu_bwd_scalar(const T* __restrict__ grad,
-                                                            const T* __restrict__ in,
-                                                            T* __restrict__ grad_in,
+template <typename T, typename S = typename T::storage>
+__global__ __launch_bounds__(kThreads) void gelu_bwd_scalar(const S* __restrict__ grad,
+                                                            const S* __restrict__ in,
+                                                            S* __restrict__ grad_in,
                                                             int64_t begin, int64_t end) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
   for (int64_t i = begin + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < end;
        i += stride)
-    Elem<T>::store(grad_in, i, Elem<T>::load(grad, i) * gelu_grad(Elem<T>::load(in, i)));
+    T::store(grad_in, i, T::load(grad, i) * gelu_grad(T::load(in, i)));
 }
 
 int scalar_grid(int64_t n) {
@@ -160,12 +130,12 @@ int scalar_grid(int64_t n) {
   return static_cast<int>(blocks < cap ? (blocks < 1 ? 1 : blocks) : cap);
 }
 
-template <typename T>
-hipError_t launch_fwd(const T* in, T* out, int64_t numel, hipStream_t stream) {
+template <typename T, typename S = typename T::storage>
+hipError_t launch_fwd(const S* in, S* out, int64_t numel, hipStream_t stream) {
   HK_CHECK_ARG(numel >= 0);
   if (numel == 0) return hipSuccess;
   HK_CHECK_ARG(in != nullptr && out != nullptr);
-  constexpr int P = Elem<T>::kPerVec;
+  constexpr int P = T::kPerVec;
   int64_t done = 0;
   if (hk::aligned16(in) && hk::aligned16(out)) {
     const int64_t nvec = numel / P;
@@ -187,13 +157,13 @@ hipError_t launch_fwd(const T* in, T* out, int64_t numel, hipStream_t stream) {
   return hipSuccess;
 }
 
-template <typename T>
-hipError_t launch_bwd(const T* grad, const T* in, T* grad_in, int64_t numel,
+template <typename T, typename S = typename T::storage>
+hipError_t launch_bwd(const S* grad, const S* in, S* grad_in, int64_t numel,
                       hipStream_t stream) {
   HK_CHECK_ARG(numel >= 0);
   if (numel == 0) return hipSuccess;
   HK_CHECK_ARG(grad != nullptr && in != nullptr && grad_in != nullptr);
-  constexpr int P = Elem<T>::kPerVec;
+  constexpr int P = T::kPerVec;
   int64_t done = 0;
   if (hk::aligned16(grad) && hk::aligned16(in) && hk::aligned16(grad_in)) {
     const int64_t nvec = numel / P;
@@ -220,18 +190,26 @@ hipError_t launch_bwd(const T* grad, const T* in, T* grad_in, int64_t numel,
 
 extern "C" hipError_t hk_gelu_forward_f32(const float* in, float* out, int64_t numel,
                                           hipStream_t stream) {
-  return launch_fwd<float>(in, out, numel, stream);
+  return launch_fwd<hk::F32>(in, out, numel, stream);
 }
 extern "C" hipError_t hk_gelu_forward_bf16(const hk_bf16* in, hk_bf16* out, int64_t numel,
                                            hipStream_t stream) {
-  return launch_fwd<uint16_t>(in, out, numel, stream);
+  return launch_fwd<hk::BF16>(in, out, numel, stream);
+}
+extern "C" hipError_t hk_gelu_forward_f16(const hk_f16* in, hk_f16* out, int64_t numel,
+                                          hipStream_t stream) {
+  return launch_fwd<hk::F16>(in, out, numel, stream);
 }
 extern "C" hipError_t hk_gelu_backward_f32(const float* grad, const float* in, float* grad_in,
                                            int64_t numel, hipStream_t stream) {
-  return launch_bwd<float>(grad, in, grad_in, numel, stream);
+  return launch_bwd<hk::F32>(grad, in, grad_in, numel, stream);
 }
 extern "C" hipError_t hk_gelu_backward_bf16(const hk_bf16* grad, const hk_bf16* in,
                                             hk_bf16* grad_in, int64_t numel,
                                             hipStream_t stream) {
-  return launch_bwd<uint16_t>(grad, in, grad_in, numel, stream);
+  return launch_bwd<hk::BF16>(grad, in, grad_in, numel, stream);
+}
+extern "C" hipError_t hk_gelu_backward_f16(const hk_f16* grad, const hk_f16* in,
+                                           hk_f16* grad_in, int64_t numel, hipStream_t stream) {
+  return launch_bwd<hk::F16>(grad, in, grad_in, numel, stream);
 }

@@ -29,6 +29,16 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
 }
 
+// ---- fp16 <-> fp32 -------------------------------------------------------------------------
+// IEEE binary16 through the hardware conversions: v_cvt_f32_f16 is exact and v_cvt_f16_f32
+// rounds to nearest even (the default mode), overflowing to inf, like __float2half_rn.
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
 // ---- streaming (non-temporal) 16-byte accesses ---------------------------------------------
 // HIP's float4 / uint4 are structs; the non-temporal builtins need native vector types.
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -49,6 +59,59 @@ __device__ __forceinline__ uint4 ld_nt(const uint4* p) {
 __device__ __forceinline__ void st_nt(uint4* p, uint4 v) {
   const u32x4_t w = {v.x, v.y, v.z, v.w};
   __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(p));
+}
+
+// ---- storage formats ----------------------------------------------------------------------
+// Tags for the element types a kernel can read and write; arithmetic is always fp32. `unpack`
+// and `pack` convert one 16-byte vector (kPerVec elements) to and from fp32 values.
+struct F32 {
+  using storage = float;
+  static constexpr int kPerVec = 4;
+  __device__ static float load(const float* p, int64_t i) { return p[i]; }
+  __device__ static void store(float* p, int64_t i, float v) { p[i] = v; }
+  __device__ static void unpack(const uint4& r, float* f) {
+    f[0] = __uint_as_float(r.x); f[1] = __uint_as_float(r.y);
+    f[2] = __uint_as_float(r.z); f[3] = __uint_as_float(r.w);
+  }
+  __device__ static uint4 pack(const float* f) {
+    return make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
+                      __float_as_uint(f[3]));
+  }
+};
+
+// 16-bit formats: element 2k of a vector is the low half of 32-bit word k.
+template <float (*ToF32)(uint16_t), uint16_t (*FromF32)(float)>
+struct Half16 {
+  using storage = uint16_t;
+  static constexpr int kPerVec = 8;
+  __device__ static float load(const uint16_t* p, int64_t i) { return ToF32(p[i]); }
+  __device__ static void store(uint16_t* p, int64_t i, float v) { p[i] = FromF32(v); }
+  __device__ static void unpack(const uint4& r, float* f) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      f[2 * k] = ToF32(static_cast<uint16_t>(w[k]));
+      f[2 * k + 1] = ToF32(static_cast<uint16_t>(w[k] >> 16));
+    }
+  }
+  __device__ static uint32_t pack2(float lo, float hi) {
+    return static_cast<uint32_t>(FromF32(lo)) | (static_cast<uint32_t>(FromF32(hi)) << 16);
+  }
+  __device__ static uint4 pack(const float* f) {
+    return make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
+  }
+};
+using BF16 = Half16<bf16_to_f32, f32_to_bf16>;
+using F16 = Half16<f16_to_f32, f32_to_f16>;
+
+// Pairwise sum of an fp32 array of length P (a power of two): ((f0 + f1) + (f2 + f3)) + ...
+template <int P>
+__device__ __forceinline__ float tree_sum(const float* f) {
+  if constexpr (P == 1) {
+    return f[0];
+  } else {
+    return tree_sum<P / 2>(f) + tree_sum<P / 2>(f + P / 2);
+  }
 }
 
 // ---- wave reductions (64 lanes, butterfly: every lane ends with the result) ----------------

@@ -1,4 +1,5 @@
-// layernorm.hip - LayerNorm forward / backward over fp32 rows [rows, cols].
+// layernorm.hip - LayerNorm forward / backward over rows [rows, cols] of fp32, bf16 or fp16
+// (statistics, gamma/beta gradients and all arithmetic in fp32).
 //
 // Reference behaviour:
 //   forward            kernels/layernorm/layer_norm_forward_sm89_kernel.cu:27-209
@@ -9,11 +10,12 @@
 //   backward (g, b)    kernels/layernorm/ln_backward_gamma_beta_sm89_kernel.cu:15-49
 //                      dgamma += sum_r dy xhat, dbeta += sum_r dy
 //
-// Design (gfx950): one 64-lane wave owns one row; for cols % 4 == 0 and cols <= 4096 the row is
-// held in VGPRs (VPL float4 per lane), so x is read from HBM exactly once and mean/variance
-// are computed in two exact passes over registers (no Welford merge needed). The gamma/beta
-// gradient is accumulated per lane in registers across the rows a wave visits, reduced across
-// the workgroup's waves in LDS, written as one partial per workgroup, and summed over the
+// Design (gfx950): one 64-lane wave owns one row; when a row is a whole number of 16-byte
+// vectors (cols % 4 == 0 for fp32, % 8 for 16-bit) of at most 16 per lane (cols <= 4096 fp32,
+// 8192 16-bit) the row is held in VGPRs in its storage format, so x is read from HBM once
+// and mean/variance are computed in two exact passes over registers (no Welford merge). The
+// gamma/beta gradient is accumulated per lane in registers across the rows a wave visits,
+// reduced across the workgroup's waves in LDS, written as one partial per workgroup, and summed over the
 // workgroups in a fixed order by a second small kernel: the result is deterministic, unlike
 // the reference's atomics. Shapes outside the register path use a workgroup-per-row fallback.
 #include <initializer_list>
@@ -27,40 +29,60 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / HK_WAVE;
 
-__device__ __forceinline__ float4 f4_zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
-__device__ __forceinline__ float f4_sum(float4 v) { return (v.x + v.y) + (v.z + v.w); }
+// Storage type of a format tag, in a form that template argument deduction does not look at.
+template <typename T>
+using St = typename T::storage;
+
+__device__ __forceinline__ uint4 u4_zero() { return make_uint4(0u, 0u, 0u, 0u); }
+
+// One 16-byte vector of gamma (or beta) as fp32, or `dflt` everywhere when the pointer is NULL.
+template <typename T>
+__device__ __forceinline__ void affine(const uint4* p, int c, float dflt, float* f) {
+  if (p) {
+    T::unpack(p[c], f);
+  } else {
+#pragma unroll
+    for (int k = 0; k < T::kPerVec; ++k) f[k] = dflt;
+  }
+}
 
 // ------------------------------------------------------------------------------------------
-// Forward, register-resident rows.
+// Forward, register-resident rows: VPL 16-byte vectors per lane, nvec vectors per row.
 // ------------------------------------------------------------------------------------------
-template <int VPL>
-__global__ __launch_bounds__(kThreads) void ln_fwd_reg(const float4* __restrict__ x,
-                                                       const float4* __restrict__ gamma,
-                                                       const float4* __restrict__ beta,
-                                                       float4* __restrict__ y,
+template <typename T, int VPL>
+__global__ __launch_bounds__(kThreads) void ln_fwd_reg(const uint4* __restrict__ x,
+                                                       const uint4* __restrict__ gamma,
+                                                       const uint4* __restrict__ beta,
+                                                       uint4* __restrict__ y,
                                                        float* __restrict__ mean_out,
                                                        float* __restrict__ rstd_out, int rows,
-                                                       int cols4, float inv_cols, float eps) {
+                                                       int nvec, float inv_cols, float eps) {
+  constexpr int P = T::kPerVec;
   const int lane = threadIdx.x & (HK_WAVE - 1);
   const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const float4* xr = x + static_cast<int64_t>(row) * cols4;
-  float4 v[VPL];
+  const uint4* xr = x + static_cast<int64_t>(row) * nvec;
+  uint4 v[VPL];
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int c = lane + i * HK_WAVE;
-    v[i] = (c < cols4) ? hk::ld_nt(xr + c) : f4_zero();
-    s += f4_sum(v[i]);
+    v[i] = (c < nvec) ? hk::ld_nt(xr + c) : u4_zero();
+    float f[P];
+    T::unpack(v[i], f);
+    s += hk::tree_sum<P>(f);
   }
   const float mu = hk::wave_sum(s) * inv_cols;
   float q = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int c = lane + i * HK_WAVE;
-    if (c < cols4) {
-      const float a = v[i].x - mu, b = v[i].y - mu, cc = v[i].z - mu, d = v[i].w - mu;
-      q += (a * a + b * b) + (cc * cc + d * d);
+    if (c < nvec) {
+      float f[P];
+      T::unpack(v[i], f);
+#pragma unroll
+      for (int k = 0; k < P; ++k) f[k] = (f[k] - mu) * (f[k] - mu);
+      q += hk::tree_sum<P>(f);
     }
   }
   const float var = hk::wave_sum(q) * inv_cols;
@@ -69,19 +91,18 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_reg(const float4* __restrict_
     if (mean_out) mean_out[row] = mu;
     if (rstd_out) rstd_out[row] = rs;
   }
-  float4* yr = y + static_cast<int64_t>(row) * cols4;
+  uint4* yr = y + static_cast<int64_t>(row) * nvec;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int c = lane + i * HK_WAVE;
-    if (c < cols4) {
-      const float4 g = gamma ? gamma[c] : make_float4(1.f, 1.f, 1.f, 1.f);
-      const float4 b = beta ? beta[c] : f4_zero();
-      float4 o;
-      o.x = (v[i].x - mu) * rs * g.x + b.x;
-      o.y = (v[i].y - mu) * rs * g.y + b.y;
-      o.z = (v[i].z - mu) * rs * g.z + b.z;
-      o.w = (v[i].w - mu) * rs * g.w + b.w;
-      hk::st_nt(yr + c, o);
+    if (c < nvec) {
+      float f[P], g[P], b[P];
+      T::unpack(v[i], f);
+      affine<T>(gamma, c, 1.f, g);
+      affine<T>(beta, c, 0.f, b);
+#pragma unroll
+      for (int k = 0; k < P; ++k) f[k] = (f[k] - mu) * rs * g[k] + b[k];
+      hk::st_nt(yr + c, T::pack(f));
     }
   }
 }
@@ -90,97 +111,126 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_reg(const float4* __restrict_
 // Backward, register-resident rows. WRITE_DX: produce grad_x. DO_GB: accumulate the
 // per-workgroup gamma/beta partials into part[blockIdx.x][2 * cols] (gamma then beta).
 // Each wave walks its rows with the next row's dy / x already in flight (software prefetch),
-// so the two wave reductions of one row overlap the loads of the next.
+// so the two wave reductions of one row overlap the loads of the next. dy, x and gamma stay
+// in registers in their storage format and are widened to fp32 where they are used.
 // ------------------------------------------------------------------------------------------
-template <int VPL, bool WRITE_DX, bool DO_GB>
+template <typename T, int VPL, bool WRITE_DX, bool DO_GB>
 __global__ __launch_bounds__(kThreads) void ln_bwd_reg(
-    const float4* __restrict__ dy, const float4* __restrict__ x, const float* __restrict__ mean,
-    const float* __restrict__ rstd, const float4* __restrict__ gamma, float4* __restrict__ dx,
-    float* __restrict__ part, int rows, int cols4, float inv_cols) {
+    const uint4* __restrict__ dy, const uint4* __restrict__ x, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const uint4* __restrict__ gamma, uint4* __restrict__ dx,
+    float* __restrict__ part, int rows, int nvec, float inv_cols) {
   // Every product below is rounded on its own (as the reference formula is written), so a
   // row whose terms cancel exactly (cols == 1) gives exactly zero.
 #pragma clang fp contract(off)
-  extern __shared__ float4 lds4[];  // [kWavesPerBlock][2][cols4] when DO_GB
+  constexpr int P = T::kPerVec;
+  extern __shared__ float4 lds4[];  // [kWavesPerBlock][2][cols] floats when DO_GB
   const int lane = threadIdx.x & (HK_WAVE - 1);
   const int wave = threadIdx.x >> 6;
-  float4 g[VPL];
-  float4 acc_g[VPL], acc_b[VPL];
+  uint4 graw[VPL];
+  float acc_g[VPL][P], acc_b[VPL][P];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int c = lane + i * HK_WAVE;
-    g[i] = (gamma && c < cols4) ? gamma[c] : make_float4(1.f, 1.f, 1.f, 1.f);
-    acc_g[i] = f4_zero();
-    acc_b[i] = f4_zero();
+    graw[i] = (gamma && c < nvec) ? gamma[c] : u4_zero();
+#pragma unroll
+    for (int k = 0; k < P; ++k) acc_g[i][k] = acc_b[i][k] = 0.f;
   }
   const int stride = gridDim.x * kWavesPerBlock;
   int row = blockIdx.x * kWavesPerBlock + wave;
-  float4 dn[VPL], xn[VPL];
+  uint4 dn[VPL], xn[VPL];
   float mn = 0.f, rn = 0.f;
   auto fetch = [&](int r) {
-    const float4* dyr = dy + static_cast<int64_t>(r) * cols4;
-    const float4* xr = x + static_cast<int64_t>(r) * cols4;
+    const uint4* dyr = dy + static_cast<int64_t>(r) * nvec;
+    const uint4* xr = x + static_cast<int64_t>(r) * nvec;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int c = lane + i * HK_WAVE;
-      dn[i] = (c < cols4) ? hk::ld_nt(dyr + c) : f4_zero();
-      xn[i] = (c < cols4) ? hk::ld_nt(xr + c) : f4_zero();
+      dn[i] = (c < nvec) ? hk::ld_nt(dyr + c) : u4_zero();
+      xn[i] = (c < nvec) ? hk::ld_nt(xr + c) : u4_zero();
     }
     mn = mean[r];
     rn = rstd[r];
   };
+  // dy, x-hat and dy * gamma of vector i of the current row (x-hat is zero past the row end).
+  auto widen = [&](const uint4& draw, const uint4& xraw, int i, float m, float rs, float* d,
+                   float* n, float* a) {
+    const bool in = lane + i * HK_WAVE < nvec;
+    float g[P];
+    T::unpack(draw, d);
+    T::unpack(xraw, n);
+    if (gamma) {
+      T::unpack(graw[i], g);
+    } else {
+#pragma unroll
+      for (int k = 0; k < P; ++k) g[k] = 1.f;
+    }
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+      n[k] = in ? (n[k] - m) * rs : 0.f;
+      a[k] = d[k] * g[k];
+    }
+  };
   if (row < rows) fetch(row);
   for (; row < rows; row += stride) {
-    float4 d[VPL], n[VPL];
+    uint4 dcur[VPL], xcur[VPL];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      d[i] = dn[i];
-      n[i] = xn[i];
+      dcur[i] = dn[i];
+      xcur[i] = xn[i];
     }
     const float m = mn, rs = rn;
     if (row + stride < rows) fetch(row + stride);
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      const bool in = lane + i * HK_WAVE < cols4;
-      n[i].x = in ? (n[i].x - m) * rs : 0.f; n[i].y = in ? (n[i].y - m) * rs : 0.f;
-      n[i].z = in ? (n[i].z - m) * rs : 0.f; n[i].w = in ? (n[i].w - m) * rs : 0.f;
+      float d[P], n[P], a[P];
+      widen(dcur[i], xcur[i], i, m, rs, d, n, a);
       if (DO_GB) {
-        acc_g[i].x += d[i].x * n[i].x; acc_g[i].y += d[i].y * n[i].y;
-        acc_g[i].z += d[i].z * n[i].z; acc_g[i].w += d[i].w * n[i].w;
-        acc_b[i].x += d[i].x; acc_b[i].y += d[i].y; acc_b[i].z += d[i].z; acc_b[i].w += d[i].w;
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+          acc_g[i][k] += d[k] * n[k];
+          acc_b[i][k] += d[k];
+        }
       }
       if (WRITE_DX) {
-        const float a0 = d[i].x * g[i].x, a1 = d[i].y * g[i].y;
-        const float a2 = d[i].z * g[i].z, a3 = d[i].w * g[i].w;
-        s1 += (a0 + a1) + (a2 + a3);
-        s2 += (a0 * n[i].x + a1 * n[i].y) + (a2 * n[i].z + a3 * n[i].w);
+        s1 += hk::tree_sum<P>(a);
+#pragma unroll
+        for (int k = 0; k < P; ++k) n[k] = a[k] * n[k];
+        s2 += hk::tree_sum<P>(n);
       }
     }
     if (WRITE_DX) {
       const float t1 = hk::wave_sum(s1), t2 = hk::wave_sum(s2);
-      float4* dxr = dx + static_cast<int64_t>(row) * cols4;
+      uint4* dxr = dx + static_cast<int64_t>(row) * nvec;
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         const int c = lane + i * HK_WAVE;
-        if (c < cols4) {
-          float4 o;
-          o.x = rs * (d[i].x * g[i].x - (t1 + n[i].x * t2) * inv_cols);
-          o.y = rs * (d[i].y * g[i].y - (t1 + n[i].y * t2) * inv_cols);
-          o.z = rs * (d[i].z * g[i].z - (t1 + n[i].z * t2) * inv_cols);
-          o.w = rs * (d[i].w * g[i].w - (t1 + n[i].w * t2) * inv_cols);
-          hk::st_nt(dxr + c, o);
+        if (c < nvec) {
+          float d[P], n[P], a[P], o[P];
+          widen(dcur[i], xcur[i], i, m, rs, d, n, a);
+#pragma unroll
+          for (int k = 0; k < P; ++k) o[k] = rs * (a[k] - (t1 + n[k] * t2) * inv_cols);
+          hk::st_nt(dxr + c, T::pack(o));
         }
       }
     }
   }
   if (DO_GB) {
+    // LDS holds [wave][gamma | beta][cols] floats; vector c covers columns c*P .. c*P+P-1.
+    constexpr int Q = P / 4;  // float4s per vector
+    const int cols4 = nvec * Q;
     float4* my = lds4 + static_cast<int64_t>(wave) * 2 * cols4;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int c = lane + i * HK_WAVE;
-      if (c < cols4) {
-        my[c] = acc_g[i];
-        my[cols4 + c] = acc_b[i];
+      if (c < nvec) {
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+          my[c * Q + q] = make_float4(acc_g[i][4 * q], acc_g[i][4 * q + 1], acc_g[i][4 * q + 2],
+                                      acc_g[i][4 * q + 3]);
+          my[cols4 + c * Q + q] = make_float4(acc_b[i][4 * q], acc_b[i][4 * q + 1],
+                                              acc_b[i][4 * q + 2], acc_b[i][4 * q + 3]);
+        }
       }
     }
     __syncthreads();
@@ -247,22 +297,23 @@ __device__ float block_sum(float v, float* red) {
   return t;
 }
 
-__global__ __launch_bounds__(kThreads) void ln_fwd_rowblock(const float* __restrict__ x,
-                                                            const float* __restrict__ gamma,
-                                                            const float* __restrict__ beta,
-                                                            float* __restrict__ y,
+template <typename T, typename S = typename T::storage>
+__global__ __launch_bounds__(kThreads) void ln_fwd_rowblock(const S* __restrict__ x,
+                                                            const S* __restrict__ gamma,
+                                                            const S* __restrict__ beta,
+                                                            S* __restrict__ y,
                                                             float* __restrict__ mean_out,
                                                             float* __restrict__ rstd_out,
                                                             int cols, float eps) {
   __shared__ float red[kWavesPerBlock];
   const int64_t row = blockIdx.x;
-  const float* xr = x + row * cols;
+  const S* xr = x + row * cols;
   float s = 0.f;
-  for (int c = threadIdx.x; c < cols; c += kThreads) s += xr[c];
+  for (int c = threadIdx.x; c < cols; c += kThreads) s += T::load(xr, c);
   const float mu = block_sum(s, red) / static_cast<float>(cols);
   float q = 0.f;
   for (int c = threadIdx.x; c < cols; c += kThreads) {
-    const float d = xr[c] - mu;
+    const float d = T::load(xr, c) - mu;
     q += d * d;
   }
   const float var = block_sum(q, red) / static_cast<float>(cols);
@@ -271,43 +322,44 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_rowblock(const float* __restr
     if (mean_out) mean_out[row] = mu;
     if (rstd_out) rstd_out[row] = rs;
   }
-  float* yr = y + row * cols;
+  S* yr = y + row * cols;
   for (int c = threadIdx.x; c < cols; c += kThreads) {
-    const float g = gamma ? gamma[c] : 1.f, b = beta ? beta[c] : 0.f;
-    yr[c] = (xr[c] - mu) * rs * g + b;
+    const float g = gamma ? T::load(gamma, c) : 1.f, b = beta ? T::load(beta, c) : 0.f;
+    T::store(yr, c, (T::load(xr, c) - mu) * rs * g + b);
   }
 }
 
+template <typename T, typename S = typename T::storage>
 __global__ __launch_bounds__(kThreads) void ln_bwd_input_rowblock(
-    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ mean,
-    const float* __restrict__ rstd, const float* __restrict__ gamma, float* __restrict__ dx,
-    int cols) {
+    const S* __restrict__ dy, const S* __restrict__ x, const float* __restrict__ mean,
+    const float* __restrict__ rstd, const S* __restrict__ gamma, S* __restrict__ dx, int cols) {
 #pragma clang fp contract(off)
   __shared__ float red[kWavesPerBlock];
   const int64_t row = blockIdx.x;
   const float m = mean[row], rs = rstd[row];
-  const float* dyr = dy + row * cols;
-  const float* xr = x + row * cols;
+  const S* dyr = dy + row * cols;
+  const S* xr = x + row * cols;
   float s1 = 0.f, s2 = 0.f;
   for (int c = threadIdx.x; c < cols; c += kThreads) {
-    const float a = dyr[c] * (gamma ? gamma[c] : 1.f);
+    const float a = T::load(dyr, c) * (gamma ? T::load(gamma, c) : 1.f);
     s1 += a;
-    s2 += a * ((xr[c] - m) * rs);
+    s2 += a * ((T::load(xr, c) - m) * rs);
   }
   const float t1 = block_sum(s1, red);
   const float t2 = block_sum(s2, red);
   const float ic = 1.0f / static_cast<float>(cols);
-  float* dxr = dx + row * cols;
+  S* dxr = dx + row * cols;
   for (int c = threadIdx.x; c < cols; c += kThreads) {
-    const float n = (xr[c] - m) * rs;
-    dxr[c] = rs * (dyr[c] * (gamma ? gamma[c] : 1.f) - (t1 + n * t2) * ic);
+    const float n = (T::load(xr, c) - m) * rs;
+    T::store(dxr, c, rs * (T::load(dyr, c) * (gamma ? T::load(gamma, c) : 1.f) - (t1 + n * t2) * ic));
   }
 }
 
 // Column-parallel gamma/beta gradient for the fallback path: one thread per column, rows
 // summed in order (deterministic).
-__global__ __launch_bounds__(kThreads) void ln_gb_columns(const float* __restrict__ dy,
-                                                          const float* __restrict__ x,
+template <typename T, typename S = typename T::storage>
+__global__ __launch_bounds__(kThreads) void ln_gb_columns(const S* __restrict__ dy,
+                                                          const S* __restrict__ x,
                                                           const float* __restrict__ mean,
                                                           const float* __restrict__ rstd,
                                                           float* __restrict__ grad_gamma,
@@ -318,8 +370,8 @@ __global__ __launch_bounds__(kThreads) void ln_gb_columns(const float* __restric
   float sg = 0.f, sb = 0.f;
   for (int r = 0; r < rows; ++r) {
     const int64_t o = static_cast<int64_t>(r) * cols + c;
-    const float d = dy[o];
-    sg += d * ((x[o] - mean[r]) * rstd[r]);
+    const float d = T::load(dy, o);
+    sg += d * ((T::load(x, o) - mean[r]) * rstd[r]);
     sb += d;
   }
   if (grad_gamma) grad_gamma[c] += sg;
@@ -351,12 +403,18 @@ hipError_t with_vpl(int vpl, F&& f) {
   }
 }
 
+template <typename T>
 bool reg_path_ok(int cols, std::initializer_list<const void*> ptrs) {
-  if (cols % 4 != 0 || pick_vpl(cols / 4) == 0) return false;
+  constexpr int P = T::kPerVec;
+  if (cols % P != 0 || pick_vpl(cols / P) == 0) return false;
   for (const void* p : ptrs)
     if (p && !hk::aligned16(p)) return false;
   return true;
 }
+
+constexpr int kMaxGbCols = 2048;
+template <typename T>
+constexpr int kMaxBwdVpl = 4096 / (HK_WAVE * T::kPerVec);
 
 int bwd_grid(int rows) {
   const int64_t want = hk::ceil_div(rows, kWavesPerBlock);
@@ -364,17 +422,46 @@ int bwd_grid(int rows) {
   return static_cast<int>(want < cap ? want : cap);
 }
 
-hipError_t launch_bwd(const float* dy, const float* x, const float* mean, const float* rstd,
-                      const float* gamma, float* dx, float* dgamma, float* dbeta, int rows,
+template <typename T>
+hipError_t launch_fwd(const St<T>* x, const St<T>* gamma, const St<T>* beta, St<T>* y,
+                      float* mean_out, float* rstd_out, int rows, int cols, float eps,
+                      hipStream_t stream) {
+  HK_CHECK_ARG(rows >= 0 && cols >= 0);
+  if (rows == 0 || cols == 0) return hipSuccess;
+  HK_CHECK_ARG(x && y);
+  if (reg_path_ok<T>(cols, {x, gamma, beta, y})) {
+    const int nvec = cols / T::kPerVec;
+    const unsigned grid = static_cast<unsigned>(hk::ceil_div(rows, kWavesPerBlock));
+    const float inv_cols = 1.0f / static_cast<float>(cols);
+    return with_vpl(pick_vpl(nvec), [&](auto vpl_c) -> hipError_t {
+      constexpr int V = decltype(vpl_c)::value;
+      hipLaunchKernelGGL((ln_fwd_reg<T, V>), dim3(grid), dim3(kThreads), 0, stream,
+                         reinterpret_cast<const uint4*>(x), reinterpret_cast<const uint4*>(gamma),
+                         reinterpret_cast<const uint4*>(beta), reinterpret_cast<uint4*>(y),
+                         mean_out, rstd_out, rows, nvec, inv_cols, eps);
+      return hk::launch_status();
+    });
+  }
+  hipLaunchKernelGGL(ln_fwd_rowblock<T>, dim3(rows), dim3(kThreads), 0, stream, x, gamma, beta, y,
+                     mean_out, rstd_out, cols, eps);
+  return hk::launch_status();
+}
+
+template <typename T>
+hipError_t launch_bwd(const St<T>* dy, const St<T>* x, const float* mean, const float* rstd,
+                      const St<T>* gamma, St<T>* dx, float* dgamma, float* dbeta, int rows,
                       int cols, bool write_dx, bool do_gb, hipStream_t stream) {
   HK_CHECK_ARG(rows >= 0 && cols >= 0);
   if (rows == 0 || cols == 0) return hipSuccess;
   HK_CHECK_ARG(dy && x && mean && rstd);
   HK_CHECK_ARG(!write_dx || dx);
   // The gamma/beta partials of one workgroup live in LDS: 4 waves x 2 x cols floats, kept
-  // within 64 KiB.
-  if (reg_path_ok(cols, {dy, x, gamma, dx}) && (!do_gb || cols <= 2048)) {
-    const int cols4 = cols / 4;
+  // within 64 KiB (cols <= kMaxGbCols). The backward keeps dy, x and their prefetch in
+  // registers; past kMaxBwdVpl vectors per lane (4096 columns for every storage type) it would
+  // spill, so wider rows take the workgroup-per-row kernels.
+  if (reg_path_ok<T>(cols, {dy, x, gamma, dx}) && pick_vpl(cols / T::kPerVec) <= kMaxBwdVpl<T> &&
+      (!do_gb || cols <= kMaxGbCols)) {
+    const int nvec = cols / T::kPerVec;
     const int grid = write_dx && !do_gb ? static_cast<int>(hk::ceil_div(rows, kWavesPerBlock))
                                         : bwd_grid(rows);
     float* part = nullptr;
@@ -386,15 +473,25 @@ hipError_t launch_bwd(const float* dy, const float* x, const float* mean, const 
     }
     const size_t lds = do_gb ? static_cast<size_t>(kWavesPerBlock) * 2 * cols * sizeof(float) : 0;
     const float inv_cols = 1.0f / static_cast<float>(cols);
-    HK_RETURN_IF_ERROR(with_vpl(pick_vpl(cols4), [&](auto vpl_c) -> hipError_t {
+    HK_RETURN_IF_ERROR(with_vpl(pick_vpl(nvec), [&](auto vpl_c) -> hipError_t {
       constexpr int V = decltype(vpl_c)::value;
-      auto* k = write_dx ? (do_gb ? ln_bwd_reg<V, true, true> : ln_bwd_reg<V, true, false>)
-                         : ln_bwd_reg<V, false, true>;
-      hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), lds, stream,
-                         reinterpret_cast<const float4*>(dy), reinterpret_cast<const float4*>(x),
-                         mean, rstd, reinterpret_cast<const float4*>(gamma),
-                         reinterpret_cast<float4*>(dx), part, rows, cols4, inv_cols);
-      return hk::launch_status();
+      // only the forms the conditions above can select are instantiated
+      if constexpr (V > kMaxBwdVpl<T>) {
+        return hipErrorInvalidValue;
+      } else {
+        constexpr bool kGb = V * HK_WAVE * T::kPerVec <= kMaxGbCols;
+        void (*k)(const uint4*, const uint4*, const float*, const float*, const uint4*, uint4*,
+                  float*, int, int, float) = ln_bwd_reg<T, V, true, false>;
+        if constexpr (kGb) {
+          if (do_gb) k = write_dx ? ln_bwd_reg<T, V, true, true> : ln_bwd_reg<T, V, false, true>;
+        }
+        if (do_gb && !kGb) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), lds, stream,
+                           reinterpret_cast<const uint4*>(dy), reinterpret_cast<const uint4*>(x),
+                           mean, rstd, reinterpret_cast<const uint4*>(gamma),
+                           reinterpret_cast<uint4*>(dx), part, rows, nvec, inv_cols);
+        return hk::launch_status();
+      }
     }));
     if (do_gb) {
       hipLaunchKernelGGL(ln_gb_finalize, dim3(static_cast<unsigned>(hk::ceil_div(2 * cols, HK_WAVE))),
@@ -404,12 +501,12 @@ hipError_t launch_bwd(const float* dy, const float* x, const float* mean, const 
     return hipSuccess;
   }
   if (write_dx) {
-    hipLaunchKernelGGL(ln_bwd_input_rowblock, dim3(rows), dim3(kThreads), 0, stream, dy, x, mean,
-                       rstd, gamma, dx, cols);
+    hipLaunchKernelGGL(ln_bwd_input_rowblock<T>, dim3(rows), dim3(kThreads), 0, stream, dy, x,
+                       mean, rstd, gamma, dx, cols);
     HK_RETURN_IF_ERROR(hk::launch_status());
   }
   if (do_gb) {
-    hipLaunchKernelGGL(ln_gb_columns, dim3(static_cast<unsigned>(hk::ceil_div(cols, kThreads))),
+    hipLaunchKernelGGL(ln_gb_columns<T>, dim3(static_cast<unsigned>(hk::ceil_div(cols, kThreads))),
                        dim3(kThreads), 0, stream, dy, x, mean, rstd, dgamma, dbeta, rows, cols);
     HK_RETURN_IF_ERROR(hk::launch_status());
   }
@@ -418,54 +515,37 @@ hipError_t launch_bwd(const float* dy, const float* x, const float* mean, const 
 
 }  // namespace
 
-extern "C" hipError_t hk_layer_norm_forward_f32(const float* x, const float* gamma,
-                                                const float* beta, float* y, float* mean_out,
-                                                float* rstd_out, int rows, int cols, float eps,
-                                                hipStream_t stream) {
-  HK_CHECK_ARG(rows >= 0 && cols >= 0);
-  if (rows == 0 || cols == 0) return hipSuccess;
-  HK_CHECK_ARG(x && y);
-  if (reg_path_ok(cols, {x, gamma, beta, y})) {
-    const int cols4 = cols / 4;
-    const unsigned grid = static_cast<unsigned>(hk::ceil_div(rows, kWavesPerBlock));
-    const float inv_cols = 1.0f / static_cast<float>(cols);
-    return with_vpl(pick_vpl(cols4), [&](auto vpl_c) -> hipError_t {
-      constexpr int V = decltype(vpl_c)::value;
-      hipLaunchKernelGGL(ln_fwd_reg<V>, dim3(grid), dim3(kThreads), 0, stream,
-                         reinterpret_cast<const float4*>(x),
-                         reinterpret_cast<const float4*>(gamma),
-                         reinterpret_cast<const float4*>(beta), reinterpret_cast<float4*>(y),
-                         mean_out, rstd_out, rows, cols4, inv_cols, eps);
-      return hk::launch_status();
-    });
+// One set of four entry points per storage type: fp32 (the float kernels), and the
+// reference's __half / __nv_bfloat16 instantiations (layer_norm_forward_sm89_kernel.cu:205-210;
+// ln_backward_input_sm89_kernel.cu:107-113; ln_backward_gamma_beta_sm89_kernel.cu:51-56).
+#define HK_LN_ENTRY_POINTS(SUFFIX, TAG, S)                                                       \
+  extern "C" hipError_t hk_layer_norm_forward_##SUFFIX(const S* x, const S* gamma,              \
+                                                       const S* beta, S* y, float* mean_out,    \
+                                                       float* rstd_out, int rows, int cols,     \
+                                                       float eps, hipStream_t stream) {         \
+    return launch_fwd<TAG>(x, gamma, beta, y, mean_out, rstd_out, rows, cols, eps, stream);     \
+  }                                                                                             \
+  extern "C" hipError_t hk_ln_backward_input_##SUFFIX(const S* grad_y, const S* x,              \
+                                                      const float* mean, const float* rstd,     \
+                                                      const S* gamma, S* grad_x, int rows,      \
+                                                      int cols, hipStream_t stream) {           \
+    return launch_bwd<TAG>(grad_y, x, mean, rstd, gamma, grad_x, nullptr, nullptr, rows, cols,  \
+                           true, false, stream);                                                \
+  }                                                                                             \
+  extern "C" hipError_t hk_ln_backward_gamma_beta_##SUFFIX(                                     \
+      const S* grad_y, const S* x, const float* mean, const float* rstd, float* grad_gamma,     \
+      float* grad_beta, int rows, int cols, hipStream_t stream) {                               \
+    HK_CHECK_ARG(grad_gamma || grad_beta || rows == 0 || cols == 0);                            \
+    return launch_bwd<TAG>(grad_y, x, mean, rstd, nullptr, nullptr, grad_gamma, grad_beta, rows, \
+                           cols, false, true, stream);                                          \
+  }                                                                                             \
+  extern "C" hipError_t hk_layer_norm_backward_##SUFFIX(                                        \
+      const S* grad_y, const S* x, const float* mean, const float* rstd, const S* gamma,        \
+      S* grad_x, float* grad_gamma, float* grad_beta, int rows, int cols, hipStream_t stream) { \
+    return launch_bwd<TAG>(grad_y, x, mean, rstd, gamma, grad_x, grad_gamma, grad_beta, rows,   \
+                           cols, true, grad_gamma || grad_beta, stream);                        \
   }
-  hipLaunchKernelGGL(ln_fwd_rowblock, dim3(rows), dim3(kThreads), 0, stream, x, gamma, beta, y,
-                     mean_out, rstd_out, cols, eps);
-  return hk::launch_status();
-}
 
-extern "C" hipError_t hk_ln_backward_input_f32(const float* grad_y, const float* x,
-                                               const float* mean, const float* rstd,
-                                               const float* gamma, float* grad_x, int rows,
-                                               int cols, hipStream_t stream) {
-  return launch_bwd(grad_y, x, mean, rstd, gamma, grad_x, nullptr, nullptr, rows, cols, true,
-                    false, stream);
-}
-
-extern "C" hipError_t hk_ln_backward_gamma_beta_f32(const float* grad_y, const float* x,
-                                                    const float* mean, const float* rstd,
-                                                    float* grad_gamma, float* grad_beta,
-                                                    int rows, int cols, hipStream_t stream) {
-  HK_CHECK_ARG(grad_gamma || grad_beta || rows == 0 || cols == 0);
-  return launch_bwd(grad_y, x, mean, rstd, nullptr, nullptr, grad_gamma, grad_beta, rows, cols,
-                    false, true, stream);
-}
-
-extern "C" hipError_t hk_layer_norm_backward_f32(const float* grad_y, const float* x,
-                                                 const float* mean, const float* rstd,
-                                                 const float* gamma, float* grad_x,
-                                                 float* grad_gamma, float* grad_beta, int rows,
-                                                 int cols, hipStream_t stream) {
-  return launch_bwd(grad_y, x, mean, rstd, gamma, grad_x, grad_gamma, grad_beta, rows, cols,
-                    true, grad_gamma || grad_beta, stream);
-}
+HK_LN_ENTRY_POINTS(f32, hk::F32, float)
+HK_LN_ENTRY_POINTS(bf16, hk::BF16, hk_bf16)
+HK_LN_ENTRY_POINTS(f16, hk::F16, hk_f16)

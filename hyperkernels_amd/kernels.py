@@ -45,15 +45,17 @@ def _dev(*ts: torch.Tensor | None) -> None:
 # GELU: gelu_forward_sm89_kernel<T> (kernels/gelu/gelu_forward_sm89_kernel.cu:35-37),
 #       gelu_backward_sm89_kernel<T> (kernels/gelu/gelu_backward_sm89_kernel.cu:44-47)
 # ----------------------------------------------------------------------------------------------
-_GELU_SUFFIX = {torch.float32: "f32", torch.bfloat16: "bf16"}
+# storage dtype -> entry-point suffix (the reference's float / __nv_bfloat16 / __half
+# instantiations of the GELU and LayerNorm kernels)
+_SUFFIX = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
 
 
 def gelu_forward(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     _dev(x, out)
     out = torch.empty_like(x) if out is None else out
-    if x.dtype not in _GELU_SUFFIX or out.dtype != x.dtype or out.numel() != x.numel():
-        raise ValueError("gelu_forward: fp32 or bf16 tensors of equal size")
-    call(f"hk_gelu_forward_{_GELU_SUFFIX[x.dtype]}", _ptr(x), _ptr(out), x.numel(), _stream())
+    if x.dtype not in _SUFFIX or out.dtype != x.dtype or out.numel() != x.numel():
+        raise ValueError("gelu_forward: fp32, bf16 or fp16 tensors of equal size")
+    call(f"hk_gelu_forward_{_SUFFIX[x.dtype]}", _ptr(x), _ptr(out), x.numel(), _stream())
     return out
 
 
@@ -61,10 +63,10 @@ def gelu_backward(grad: torch.Tensor, x: torch.Tensor,
                   grad_in: torch.Tensor | None = None) -> torch.Tensor:
     _dev(grad, x, grad_in)
     grad_in = torch.empty_like(x) if grad_in is None else grad_in
-    if x.dtype not in _GELU_SUFFIX or not (grad.dtype == x.dtype == grad_in.dtype) or not (
+    if x.dtype not in _SUFFIX or not (grad.dtype == x.dtype == grad_in.dtype) or not (
             grad.numel() == x.numel() == grad_in.numel()):
-        raise ValueError("gelu_backward: fp32 or bf16 tensors of equal size")
-    call(f"hk_gelu_backward_{_GELU_SUFFIX[x.dtype]}", _ptr(grad), _ptr(x), _ptr(grad_in),
+        raise ValueError("gelu_backward: fp32, bf16 or fp16 tensors of equal size")
+    call(f"hk_gelu_backward_{_SUFFIX[x.dtype]}", _ptr(grad), _ptr(x), _ptr(grad_in),
          x.numel(), _stream())
     return grad_in
 
@@ -79,8 +81,20 @@ def _rows_cols(x: torch.Tensor) -> tuple[int, int]:
     return (x.numel() // cols if cols else 0), cols
 
 
+def _ln_suffix(data, stats) -> str:
+    """Entry-point suffix for LayerNorm: `data` tensors (x, gamma, beta, y, dy, dx) share one
+    storage dtype; `stats` tensors (mean, rstd, grad_gamma, grad_beta) are fp32."""
+    dt = data[0].dtype
+    if dt not in _SUFFIX or any(t is not None and t.dtype != dt for t in data):
+        raise ValueError("layer norm: x, gamma, beta, y, dy and dx must share one dtype "
+                         "(fp32, bf16 or fp16)")
+    if any(t is not None and t.dtype != torch.float32 for t in stats):
+        raise ValueError("layer norm: mean, rstd, grad_gamma and grad_beta are fp32")
+    return _SUFFIX[dt]
+
+
 def layer_norm_forward(x, gamma=None, beta=None, eps: float = 1e-5, y=None, mean=None, rstd=None):
-    """layer_norm_forward_sm89_kernel<float,float> (layer_norm_forward_sm89_kernel.cu:27-32).
+    """layer_norm_forward_sm89_kernel<T,float> (layer_norm_forward_sm89_kernel.cu:27-32).
 
     Returns (y, mean, rstd); mean/rstd are [rows] fp32."""
     _dev(x, gamma, beta, y, mean, rstd)
@@ -88,29 +102,32 @@ def layer_norm_forward(x, gamma=None, beta=None, eps: float = 1e-5, y=None, mean
     y = torch.empty_like(x) if y is None else y
     mean = torch.empty(rows, device=x.device, dtype=torch.float32) if mean is None else mean
     rstd = torch.empty(rows, device=x.device, dtype=torch.float32) if rstd is None else rstd
-    call("hk_layer_norm_forward_f32", _ptr(x), _ptr(gamma), _ptr(beta), _ptr(y), _ptr(mean),
+    sfx = _ln_suffix([x, gamma, beta, y], [mean, rstd])
+    call(f"hk_layer_norm_forward_{sfx}", _ptr(x), _ptr(gamma), _ptr(beta), _ptr(y), _ptr(mean),
          _ptr(rstd), rows, cols, ctypes.c_float(eps), _stream())
     return y, mean, rstd
 
 
 def ln_backward_input(grad_y, x, mean, rstd, gamma=None, grad_x=None):
-    """OwnTensor::cuda::ln_backward_input_sm89_kernel<float> (ln_backward_input_sm89_kernel.cu:33-38)."""
+    """OwnTensor::cuda::ln_backward_input_sm89_kernel<T> (ln_backward_input_sm89_kernel.cu:33-38)."""
     _dev(grad_y, x, mean, rstd, gamma, grad_x)
     rows, cols = _rows_cols(x)
     grad_x = torch.empty_like(x) if grad_x is None else grad_x
-    call("hk_ln_backward_input_f32", _ptr(grad_y), _ptr(x), _ptr(mean), _ptr(rstd), _ptr(gamma),
-         _ptr(grad_x), rows, cols, _stream())
+    sfx = _ln_suffix([x, grad_y, gamma, grad_x], [mean, rstd])
+    call(f"hk_ln_backward_input_{sfx}", _ptr(grad_y), _ptr(x), _ptr(mean), _ptr(rstd),
+         _ptr(gamma), _ptr(grad_x), rows, cols, _stream())
     return grad_x
 
 
 def ln_backward_gamma_beta(grad_y, x, mean, rstd, grad_gamma, grad_beta):
-    """ln_backward_gamma_beta_sm89_kernel<float> (ln_backward_gamma_beta_sm89_kernel.cu:15-21).
+    """ln_backward_gamma_beta_sm89_kernel<T> (ln_backward_gamma_beta_sm89_kernel.cu:15-21).
 
     ADDS the column sums into grad_gamma / grad_beta (the reference's atomics into caller-zeroed
     buffers), in a fixed order."""
     _dev(grad_y, x, mean, rstd, grad_gamma, grad_beta)
     rows, cols = _rows_cols(x)
-    call("hk_ln_backward_gamma_beta_f32", _ptr(grad_y), _ptr(x), _ptr(mean), _ptr(rstd),
+    sfx = _ln_suffix([x, grad_y], [mean, rstd, grad_gamma, grad_beta])
+    call(f"hk_ln_backward_gamma_beta_{sfx}", _ptr(grad_y), _ptr(x), _ptr(mean), _ptr(rstd),
          _ptr(grad_gamma), _ptr(grad_beta), rows, cols, _stream())
     return grad_gamma, grad_beta
 
@@ -120,7 +137,8 @@ def layer_norm_backward(grad_y, x, mean, rstd, gamma, grad_gamma, grad_beta, gra
     _dev(grad_y, x, mean, rstd, gamma, grad_gamma, grad_beta, grad_x)
     rows, cols = _rows_cols(x)
     grad_x = torch.empty_like(x) if grad_x is None else grad_x
-    call("hk_layer_norm_backward_f32", _ptr(grad_y), _ptr(x), _ptr(mean), _ptr(rstd),
+    sfx = _ln_suffix([x, grad_y, gamma, grad_x], [mean, rstd, grad_gamma, grad_beta])
+    call(f"hk_layer_norm_backward_{sfx}", _ptr(grad_y), _ptr(x), _ptr(mean), _ptr(rstd),
          _ptr(gamma), _ptr(grad_x), _ptr(grad_gamma), _ptr(grad_beta), rows, cols, _stream())
     return grad_x
 
@@ -128,33 +146,42 @@ def layer_norm_backward(grad_y, x, mean, rstd, gamma, grad_gamma, grad_beta, gra
 # ----------------------------------------------------------------------------------------------
 # Sparse cross-entropy (kernels/loss/*.cu)
 # ----------------------------------------------------------------------------------------------
+# target dtype -> entry-point suffix: the reference's <float, int32_t | int64_t | uint16_t>
+# instantiations (sparse_ce_forward_...cu:108-113; sparseCENormalize_from_stats.cu:52-60)
+_CE_INDEX = {torch.int32: "i32", torch.int64: "i64", torch.uint16: "u16"}
+
+
 def sparse_ce_forward(logits, targets, losses=None, saved_max=None, saved_sum=None):
-    """sparse_ce_forward_kernel_vec_save_stats<float,int32_t> (sparse_ce_forward_...cu:14-23).
+    """sparse_ce_forward_kernel_vec_save_stats<float,TIdx> (sparse_ce_forward_...cu:14-23).
 
     Returns (losses, saved_max, saved_sum), each [rows] fp32."""
     _dev(logits, targets, losses, saved_max, saved_sum)
-    if logits.dtype != torch.float32 or targets.dtype != torch.int32 or logits.dim() != 2:
-        raise ValueError("sparse_ce_forward: fp32 logits [rows, vocab] and int32 targets")
+    if logits.dtype != torch.float32 or targets.dtype not in _CE_INDEX or logits.dim() != 2:
+        raise ValueError("sparse_ce_forward: fp32 logits [rows, vocab] and int32/int64/uint16 "
+                         "targets")
     rows, vocab = logits.shape
     mk = lambda: torch.empty(rows, device=logits.device, dtype=torch.float32)  # noqa: E731
     losses = mk() if losses is None else losses
     saved_max = mk() if saved_max is None else saved_max
     saved_sum = mk() if saved_sum is None else saved_sum
-    call("hk_sparse_ce_forward_f32_i32", _ptr(logits), _ptr(targets), _ptr(losses),
-         _ptr(saved_max), _ptr(saved_sum), rows, vocab, _stream())
+    call("hk_sparse_ce_forward_f32_" + _CE_INDEX[targets.dtype], _ptr(logits), _ptr(targets),
+         _ptr(losses), _ptr(saved_max), _ptr(saved_sum), rows, vocab, _stream())
     return losses, saved_max, saved_sum
 
 
 def sparse_ce_backward(logits, targets, saved_max, saved_sum, grad_output=None,
                        host_scale: float = 1.0, grad=None):
-    """sparseCENormalize_from_stats<float,int32_t> (sparseCENormalize_from_stats.cu:7-17).
+    """sparseCENormalize_from_stats<float,TIdx> (sparseCENormalize_from_stats.cu:7-17).
 
     grad_output is a 1-element device tensor (or None for 1.0)."""
     _dev(logits, targets, saved_max, saved_sum, grad_output, grad)
+    if logits.dtype != torch.float32 or targets.dtype not in _CE_INDEX or logits.dim() != 2:
+        raise ValueError("sparse_ce_backward: fp32 logits [rows, vocab] and int32/int64/uint16 "
+                         "targets")
     rows, vocab = logits.shape
     grad = torch.empty_like(logits) if grad is None else grad
-    call("hk_sparse_ce_backward_f32_i32", _ptr(logits), _ptr(targets), _ptr(grad),
-         _ptr(saved_max), _ptr(saved_sum), rows, vocab, _ptr(grad_output),
+    call("hk_sparse_ce_backward_f32_" + _CE_INDEX[targets.dtype], _ptr(logits), _ptr(targets),
+         _ptr(grad), _ptr(saved_max), _ptr(saved_sum), rows, vocab, _ptr(grad_output),
          ctypes.c_float(host_scale), _stream())
     return grad
 

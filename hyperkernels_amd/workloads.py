@@ -2,8 +2,8 @@
 
 Byte and FLOP conventions follow the reference's published numbers (back-derived from its
 README latency x throughput, README.md:186-199): attention fwd FLOP = 4 B H T^2 d (halved when
-causal), bwd = 2.5x fwd; LN fwd bytes = 2 N C 4, bwd = 3 N C 4; GELU fwd = 2 n sizeof(T),
-bwd = 3 n sizeof(T); CE fwd = R V 4, bwd = 2 R V 4; reduce = R V 4; AdamW = 7 P 4;
+causal), bwd = 2.5x fwd; LN fwd bytes = 2 N C sizeof(T), bwd = 3 N C sizeof(T);
+GELU fwd = 2 n sizeof(T), bwd = 3 n sizeof(T); CE fwd = R V 4, bwd = 2 R V 4; reduce = R V 4; AdamW = 7 P 4;
 GEMM = 2 M N K per batch.
 """
 from __future__ import annotations
@@ -42,12 +42,12 @@ BGEMM = dict(M=8192, K=1280, N=5120)                           # configs[4]
 SGEMM = dict(M=4096, N=4096, K=4096, split_k=4)                # configs[4]
 
 
-def ln_fwd_bytes(rows, cols):
-    return 2 * rows * cols * 4
+def ln_fwd_bytes(rows, cols, esize=4):
+    return 2 * rows * cols * esize
 
 
-def ln_bwd_bytes(rows, cols):
-    return 3 * rows * cols * 4
+def ln_bwd_bytes(rows, cols, esize=4):
+    return 3 * rows * cols * esize
 
 
 def gelu_fwd_bytes(n, esize):

@@ -9,7 +9,8 @@
  *
  * Conventions shared by every entry point:
  *   - All pointers are device pointers (HBM) unless stated otherwise; the caller owns them.
- *   - bf16 tensors and scalars are passed as raw bit patterns (`hk_bf16` = uint16_t).
+ *   - bf16 and fp16 tensors and scalars are passed as raw bit patterns (`hk_bf16`,
+ *     `hk_f16` = uint16_t).
  *   - Matrices are row-major, as in the reference harnesses.
  *   - The return value is the launch status. Nothing synchronises the stream.
  *   - Preconditions that the kernels still need are validated and reported as
@@ -36,6 +37,7 @@ extern "C" {
 #endif
 
 typedef uint16_t hk_bf16;
+typedef uint16_t hk_f16; /* IEEE binary16 bit pattern (__half) */
 
 /* ------------------------------------------------------------------------------------------
  * Library
@@ -61,6 +63,12 @@ HK_API hipError_t hk_gelu_backward_f32(const float* grad, const float* in, float
                                 int64_t numel, hipStream_t stream);
 HK_API hipError_t hk_gelu_backward_bf16(const hk_bf16* grad, const hk_bf16* in, hk_bf16* grad_in,
                                  int64_t numel, hipStream_t stream);
+/* fp16 forms: the reference's <__half> instantiations (gelu_forward_sm89_kernel.cu:79;
+ * gelu_backward_sm89_kernel.cu:89). fp32 math, results rounded to nearest even. */
+HK_API hipError_t hk_gelu_forward_f16(const hk_f16* in, hk_f16* out, int64_t numel,
+                               hipStream_t stream);
+HK_API hipError_t hk_gelu_backward_f16(const hk_f16* grad, const hk_f16* in, hk_f16* grad_in,
+                                int64_t numel, hipStream_t stream);
 
 /* ------------------------------------------------------------------------------------------
  * LayerNorm, fp32.
@@ -91,6 +99,41 @@ HK_API hipError_t hk_layer_norm_backward_f32(const float* grad_y, const float* x
                                       float* grad_gamma, float* grad_beta, int rows, int cols,
                                       hipStream_t stream);
 
+/* The same four entry points for bf16 and fp16 tensors, replacing the reference's
+ * <__nv_bfloat16, float> and <__half, float> instantiations
+ *   (layer_norm_forward_sm89_kernel.cu:207-210; ln_backward_input_sm89_kernel.cu:109-113;
+ *   ln_backward_gamma_beta_sm89_kernel.cu:53-56).
+ * x, gamma, beta, y, grad_y and grad_x are 16-bit; mean, rstd, grad_gamma and grad_beta are
+ * fp32, as in the reference. All arithmetic is fp32; y and grad_x are rounded to nearest even. */
+HK_API hipError_t hk_layer_norm_forward_bf16(const hk_bf16* x, const hk_bf16* gamma, const hk_bf16* beta,
+                                      hk_bf16* y, float* mean_out, float* rstd_out, int rows,
+                                      int cols, float eps, hipStream_t stream);
+HK_API hipError_t hk_ln_backward_input_bf16(const hk_bf16* grad_y, const hk_bf16* x, const float* mean,
+                                     const float* rstd, const hk_bf16* gamma, hk_bf16* grad_x,
+                                     int rows, int cols, hipStream_t stream);
+HK_API hipError_t hk_ln_backward_gamma_beta_bf16(const hk_bf16* grad_y, const hk_bf16* x,
+                                          const float* mean, const float* rstd,
+                                          float* grad_gamma, float* grad_beta, int rows,
+                                          int cols, hipStream_t stream);
+HK_API hipError_t hk_layer_norm_backward_bf16(const hk_bf16* grad_y, const hk_bf16* x, const float* mean,
+                                       const float* rstd, const hk_bf16* gamma, hk_bf16* grad_x,
+                                       float* grad_gamma, float* grad_beta, int rows, int cols,
+                                       hipStream_t stream);
+HK_API hipError_t hk_layer_norm_forward_f16(const hk_f16* x, const hk_f16* gamma, const hk_f16* beta,
+                                      hk_f16* y, float* mean_out, float* rstd_out, int rows,
+                                      int cols, float eps, hipStream_t stream);
+HK_API hipError_t hk_ln_backward_input_f16(const hk_f16* grad_y, const hk_f16* x, const float* mean,
+                                     const float* rstd, const hk_f16* gamma, hk_f16* grad_x,
+                                     int rows, int cols, hipStream_t stream);
+HK_API hipError_t hk_ln_backward_gamma_beta_f16(const hk_f16* grad_y, const hk_f16* x,
+                                          const float* mean, const float* rstd,
+                                          float* grad_gamma, float* grad_beta, int rows,
+                                          int cols, hipStream_t stream);
+HK_API hipError_t hk_layer_norm_backward_f16(const hk_f16* grad_y, const hk_f16* x, const float* mean,
+                                       const float* rstd, const hk_f16* gamma, hk_f16* grad_x,
+                                       float* grad_gamma, float* grad_beta, int rows, int cols,
+                                       hipStream_t stream);
+
 /* ------------------------------------------------------------------------------------------
  * Sparse cross-entropy over fp32 logits [batch_size, vocab_size] with int32 targets.
  * Forward replaces sparse_ce_forward_kernel_vec_save_stats<float,int32_t>
@@ -107,6 +150,30 @@ HK_API hipError_t hk_sparse_ce_forward_f32_i32(const float* logits, const int32_
                                         int64_t batch_size, int64_t vocab_size,
                                         hipStream_t stream);
 HK_API hipError_t hk_sparse_ce_backward_f32_i32(const float* logits, const int32_t* targets,
+                                         float* grad, const float* saved_max,
+                                         const float* saved_sum, int64_t batch_size,
+                                         int64_t vocab_size, const float* grad_output,
+                                         float host_scale, hipStream_t stream);
+
+/* The same two kernels with int64 and uint16 targets, replacing the reference's
+ * <float,int64_t> and <float,uint16_t> instantiations
+ *   (sparse_ce_forward_kernel_vec_save_stats.cu:110-113; sparseCENormalize_from_stats.cu:55-60).
+ * Arguments and results are as for the int32 forms; the target is widened to int64 before the
+ * range check, so a negative int64 target also gives a NaN loss. */
+HK_API hipError_t hk_sparse_ce_forward_f32_i64(const float* logits, const int64_t* targets,
+                                        float* losses, float* saved_max, float* saved_sum,
+                                        int64_t batch_size, int64_t vocab_size,
+                                        hipStream_t stream);
+HK_API hipError_t hk_sparse_ce_backward_f32_i64(const float* logits, const int64_t* targets,
+                                         float* grad, const float* saved_max,
+                                         const float* saved_sum, int64_t batch_size,
+                                         int64_t vocab_size, const float* grad_output,
+                                         float host_scale, hipStream_t stream);
+HK_API hipError_t hk_sparse_ce_forward_f32_u16(const float* logits, const uint16_t* targets,
+                                        float* losses, float* saved_max, float* saved_sum,
+                                        int64_t batch_size, int64_t vocab_size,
+                                        hipStream_t stream);
+HK_API hipError_t hk_sparse_ce_backward_f32_u16(const float* logits, const uint16_t* targets,
                                          float* grad, const float* saved_max,
                                          const float* saved_sum, int64_t batch_size,
                                          int64_t vocab_size, const float* grad_output,

@@ -102,6 +102,35 @@ def test_bf16_rounding_matches_torch(orc):
         torch.bfloat16).float().numpy())
 
 
+def test_fp16_rounding_is_ieee_rne():
+    # The 16-bit parity checks take numpy's fp32 -> fp16 conversion as RNE(ref). Pin it on the
+    # cases that separate round-to-nearest-even from truncation or round-half-up: ties at
+    # normal and subnormal spacing, the overflow threshold, and agreement with torch.
+    x = np.array([1 + 2 ** -11, 1 + 3 * 2 ** -11, 1 + 2 ** -11 + 2 ** -20, 2.0 ** -25,
+                  3 * 2.0 ** -25, 65519.0, 65520.0, -65520.0, 2.0 ** -24], np.float32)
+    want = np.array([1.0, 1 + 2 ** -9, 1 + 2 ** -10, 0.0, 2.0 ** -23, 65504.0, np.inf, -np.inf,
+                     2.0 ** -24])
+    with np.errstate(over="ignore"):  # 65520 -> inf is the case being pinned
+        np.testing.assert_array_equal(x.astype(np.float16).astype(np.float64), want)
+    y = np.random.default_rng(3).standard_normal(4096).astype(np.float32) * 100
+    np.testing.assert_array_equal(y.astype(np.float16).view(np.uint16),
+                                  torch.from_numpy(y).half().numpy().view(np.uint16))
+
+
+def test_half_ulp_check_accepts_rounding_and_rejects_one_ulp(orc):
+    from conftest import half_ulp_check
+
+    ref = orc.normal(4096, 13)
+    for fmt, bits in (("f16", ref.astype(np.float16).view(np.uint16)),
+                      ("bf16", orc.f32_to_bf16(ref))):
+        assert half_ulp_check(bits, ref, fmt)[0] == 0
+        off = bits.copy()
+        i = int(np.argmax(np.abs(ref)))
+        off[i] += 2  # two ulps away from the rounding of the largest element
+        with pytest.raises(AssertionError):
+            half_ulp_check(off, ref, fmt, rel_tol=0.0)
+
+
 # ---------------------------------------------------------------------------------------------
 # GELU
 # ---------------------------------------------------------------------------------------------
