@@ -268,6 +268,23 @@ __global__ __launch_bounds__(256) void attn_precompute_d_kernel(hk_attn_bwd_para
   if (row < p.T && sub == 0) p.D[b * p.d_strideB + h * p.d_strideH + row] = s;
 }
 
+// Any strides: one lane per element pair, 16 lanes per row, scalar loads.
+__global__ __launch_bounds__(256) void attn_precompute_d_scalar(hk_attn_bwd_params p, int hd) {
+  const int bh = blockIdx.y;
+  const int b = bh / p.nh, h = bh - b * p.nh;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  float s = 0.f;
+  if (row < p.T) {
+    const float* o = p.O + b * p.o_strideB + h * p.o_strideH + row * p.o_strideM;
+    const float* d = p.dO + b * p.do_strideB + h * p.do_strideH + row * p.do_strideM;
+    for (int k = sub; k < hd; k += 16) s += o[k] * d[k];
+  }
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 16);
+  if (row < p.T && sub == 0) p.D[b * p.d_strideB + h * p.d_strideH + row] = s;
+}
+
 bool rows_aligned(const void* base, int64_t strideB, int64_t strideH, int64_t strideM) {
   return hk::aligned16(base) && strideB % 4 == 0 && strideH % 4 == 0 && strideM % 4 == 0;
 }
@@ -307,16 +324,19 @@ extern "C" hipError_t hk_attn_bwd_precompute_D(const hk_attn_bwd_params* params,
                                                hipStream_t stream) {
   HK_CHECK_ARG(params != nullptr);
   const hk_attn_bwd_params& p = *params;
-  // the reference instantiates HeadDim in {16, 32, 64, 128, 256} (precompute_D…:93-102)
-  HK_CHECK_ARG(head_dim > 0 && head_dim % 4 == 0 && head_dim <= 256);
+  // The reference instantiates HeadDim in {16, 32, 48, 64, 80, 96, 128, 160, 192, 256}
+  // (precompute_D…:93-102); any head_dim in [1, 256] is accepted here. Rows whose start is
+  // 16-byte aligned with head_dim % 4 == 0 take 16-byte loads, anything else scalar loads.
+  HK_CHECK_ARG(head_dim > 0 && head_dim <= 256);
   HK_CHECK_ARG(p.B >= 0 && p.nh >= 0 && p.T >= 0);
   if (p.B == 0 || p.nh == 0 || p.T == 0) return hipSuccess;
   HK_CHECK_ARG(p.O && p.dO && p.D);
-  HK_CHECK_ARG(rows_aligned(p.O, p.o_strideB, p.o_strideH, p.o_strideM) &&
-               rows_aligned(p.dO, p.do_strideB, p.do_strideH, p.do_strideM));
   const int64_t bh = static_cast<int64_t>(p.B) * p.nh;
   HK_CHECK_ARG(bh <= 65535);
-  hipLaunchKernelGGL(attn_precompute_d_kernel,
+  const bool vec = head_dim % 4 == 0 &&
+                   rows_aligned(p.O, p.o_strideB, p.o_strideH, p.o_strideM) &&
+                   rows_aligned(p.dO, p.do_strideB, p.do_strideH, p.do_strideM);
+  hipLaunchKernelGGL(vec ? attn_precompute_d_kernel : attn_precompute_d_scalar,
                      dim3(static_cast<unsigned>((p.T + 15) / 16), static_cast<unsigned>(bh)),
                      dim3(256), 0, stream, p, head_dim);
   return hk::launch_status();

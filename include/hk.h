@@ -374,7 +374,8 @@ HK_API hipError_t hk_sgemm_layout(int layout, int M, int N, int K, float alpha, 
  *   O = softmax(scale Q K^T [+ causal mask j <= i]) V, LSE = max + ln(sum of exp).
  *   dropout_p must be 0 (the dropout path, :321-323, is not provided).
  * hk_attn_bwd_precompute_D replaces mem_efficient_bwd_precompute_D_sm89<HeadDim> (:45-91):
- *   D = rowsum(dO * O); head_dim any multiple of 4 up to 256.
+ *   D = rowsum(dO * O); any head_dim in [1, 256] (the reference instantiates 16, 32, 48, 64,
+ *   80, 96, 128, 160, 192 and 256, :93-102) and any O / dO strides (unit last-dim stride).
  * hk_attn_backward replaces OwnTensor::mem_efficient_bwd_unified_kernel_exp12<64, Causal>
  *   (mem_efficient_bwd_unified_kernel_exp12.cu:54-56): from Q, K, V, dO, LSE and D it WRITES
  *   dK and dV and ADDS into dQ (dQ accumulates atomically across key tiles, as in the

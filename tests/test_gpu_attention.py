@@ -181,3 +181,33 @@ def test_attn_precompute_D(hk, orc):
     torch.cuda.synchronize()
     ref = orc.attn_precompute_D(do, o)
     assert max_rel(Dt.cpu().numpy(), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("hd", [16, 32, 48, 64, 80, 96, 128, 160, 192, 256, 20, 7])
+def test_attn_precompute_D_head_dims(hk, orc, hd):
+    # Every HeadDim the reference instantiates (precompute_D...:93-102), plus two it does not
+    # (20: vector path with a partial last 64-float span; 7: scalar path), at a ragged T.
+    B, H, T = 2, 3, 77
+    say("precompute D head_dim", hd)
+    do = orc.rand_uniform(B * H * T * hd, 19).reshape(B, H, T, hd)
+    o = orc.rand_uniform(B * H * T * hd, 20).reshape(B, H, T, hd)
+    Dt = hk.attn_bwd_precompute_D(torch.from_numpy(do).to(DEV), torch.from_numpy(o).to(DEV))
+    torch.cuda.synchronize()
+    assert max_rel(Dt.cpu().numpy(), orc.attn_precompute_D(do, o)) <= 1e-5
+
+
+def test_attn_precompute_D_strided_rows(hk, orc):
+    # Rows padded to 65 floats (a stride that is not a multiple of 4) and the heads of a packed
+    # [B, T, H, d] tensor: the reference takes any strides, so must this entry point.
+    B, H, T, hd = 2, 4, 50, 64
+    say("precompute D strided")
+    do = orc.rand_uniform(B * H * T * hd, 21).reshape(B, H, T, hd)
+    o = orc.rand_uniform(B * H * T * hd, 22).reshape(B, H, T, hd)
+    ref = orc.attn_precompute_D(do, o)
+    pad = torch.zeros(B, H, T, hd + 1, device=DEV)
+    pad[..., :hd] = torch.from_numpy(do).to(DEV)
+    packed = torch.from_numpy(np.ascontiguousarray(o.transpose(0, 2, 1, 3))).to(DEV)
+    Dt = hk.attn_bwd_precompute_D(pad[..., :hd], packed.permute(0, 2, 1, 3))
+    torch.cuda.synchronize()
+    assert max_rel(Dt.cpu().numpy(), ref) <= 1e-5
+
