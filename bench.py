@@ -253,6 +253,7 @@ def per_kernel_suite(flush):
     cases.append(("reduce_inner_16384x50304", lambda: hk.unified_reduce_sum(rs, lay, rdst),
                   16384 * 50304 * 4, "hbm"))
     cases += gemm_cases(g)
+    cases += gemv_cases(g)
     cases += attention_cases(g)
     for name, fn, work, bound in cases:
         t = time_kernel(fn, ARGS.reps, flush)
@@ -287,6 +288,37 @@ def attention_cases(g):
                       lambda c=causal, lse=lse, Dt=Dt, dq=dq, dk=dk, dv=dv: hk.attn_backward(
                           q, k, v, do, lse, Dt, c, dq=dq, dk=dk, dv=dv),
                       W.attn_bwd_flop(B, H, T, D, causal), "fp32_matrix"))
+    return cases
+
+
+def gemv_cases(g):
+    """BF16 GEMV (the M == 1 products) at GPT-2 decode shapes: logits = x wte^T (nt_row,
+    [50257, 768] weight) and x W for a [4096, 16384] weight (nn_row). HBM-bound: the weight
+    is read once (2 K N bytes)."""
+    import ctypes
+
+    lib = hk.lib()
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    one, zero = 0x3F80, 0
+    cases = []
+    V, C = 50257, 768
+    x = torch.randn(C, generator=g, device=DEV).to(torch.bfloat16)
+    wte = (torch.randn(V, C, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    logits = torch.empty(V, device=DEV, dtype=torch.bfloat16)
+
+    def run_nt():
+        assert lib.hk_bgemv_nt_row(V, C, one, x.data_ptr(), wte.data_ptr(), C, zero,
+                                   logits.data_ptr(), 1, 0, 0, 0, stream()) == 0
+    cases.append(("bgemv_nt_row_50257x768", run_nt, 2 * V * C + 2 * (V + C), "hbm"))
+    K, N = 4096, 16384
+    xk = torch.randn(K, generator=g, device=DEV).to(torch.bfloat16)
+    w = (torch.randn(K, N, generator=g, device=DEV) * K ** -0.5).to(torch.bfloat16)
+    y = torch.empty(N, device=DEV, dtype=torch.bfloat16)
+
+    def run_nn():
+        assert lib.hk_bgemv_nn_row(N, K, one, xk.data_ptr(), w.data_ptr(), N, zero, y.data_ptr(),
+                                   1, 0, 0, 0, stream()) == 0
+    cases.append(("bgemv_nn_row_4096x16384", run_nn, 2 * K * N + 2 * (K + N), "hbm"))
     return cases
 
 

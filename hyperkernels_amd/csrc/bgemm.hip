@@ -551,6 +551,15 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
   const bool ta = transA != 0, tb = transB != 0;  // OP_C is OP_T for real bf16
   HK_CHECK_ARG(K == 0 || (A != nullptr && B != nullptr));
   HK_CHECK_ARG(lda >= (ta ? M : K) && ldb >= (tb ? K : N));
+  if (!bias && splitK == 0 && (M == 1 || N == 1)) {
+    // A one-row or one-column product streams one operand once: the GEMV kernels
+    if (M == 1)  // C[0][n] = sum_k op(A)[0][k] op(B)[k][n]
+      return hk::bgemv_run(tb, N, K, alpha_bits, beta_bits, B, ldb, strideB, A, ta ? lda : 1,
+                           strideA, C, 1, strideC, batchCount, stream);
+    // C[m][0] = sum_k op(A)[m][k] op(B)[k][0]
+    return hk::bgemv_run(!ta, M, K, alpha_bits, beta_bits, A, lda, strideA, B, tb ? 1 : ldb,
+                         strideB, C, ldc, strideC, batchCount, stream);
+  }
   Epi ep{bf16_bits_to_float(alpha_bits), bf16_bits_to_float(beta_bits), bias, 0, 0};
   if (bias) {
     if (bias_numel == N) ep.bcol = 1;

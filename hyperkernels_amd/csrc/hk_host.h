@@ -30,6 +30,16 @@ int device_cu_count();
 // it once per call; growing it first waits for the work queued on that stream.
 hipError_t device_workspace(size_t bytes, hipStream_t stream, void** out);
 
+// Batched BF16 matrix-vector product (bgemv.hip), shared by the hk_bgemv_* entry points and
+// hk_bgemm's M == 1 / N == 1 products. Per batch b (element strides sm, sx, sy):
+//   dot_form:  y[r*incy] = alpha sum_k mtx[r*ld + k] x[k*incx] + beta y[r*incy]
+//   otherwise: y[r*incy] = alpha sum_k x[k*incx] mtx[k*ld + r] + beta y[r*incy]
+// for r < R; y is not read when beta == 0.
+hipError_t bgemv_run(bool dot_form, int R, int K, hk_bf16 alpha, hk_bf16 beta,
+                     const hk_bf16* mtx, int64_t ld, int64_t sm, const hk_bf16* x, int64_t incx,
+                     int64_t sx, hk_bf16* y, int64_t incy, int64_t sy, int batch,
+                     hipStream_t stream);
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 

@@ -298,6 +298,33 @@ HK_API hipError_t hk_bgemm_tn_backward(int M, int N, int K, hk_bf16 alpha, const
                                        long long strideB, hk_bf16 beta, hk_bf16* C, int ldc,
                                        long long strideC, int batchCount, hipStream_t stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Batched BF16 GEMV, the M == 1 / N == 1 GEMMs, fp32 accumulation, one bf16 rounding.
+ * Replace the four kernels of blas/bf16/bgemv_sm89_kernel.cu, same arguments in the same order
+ * (the reference's Beta0 template instantiations are beta == 0 here, where C is not read):
+ *   hk_bgemv_nn_row  bgemv_nn_row_vec8_kernel<Beta0> (:11-57):  C[n] = a sum_k A[k] B[k*ldb+n]
+ *   hk_bgemv_nt_row  bgemv_nt_row_kernel<Beta0>      (:60-107): C[n] = a sum_k A[k] B[n*ldb+k]
+ *   hk_bgemv_tn_row  bgemv_tn_row_vec8_kernel<Beta0> (:110-156): C[n] = a sum_k A[k*lda] B[k*ldb+n]
+ *   hk_bgemv_nn_col  bgemv_nn_col_kernel<Beta0>      (:159-208): C[m] = a sum_k A[m*lda+k] B[k]
+ *   (+ beta C[.] when beta != 0), for each of batchCount batches with element strides sA, sB,
+ *   sC. Any N, M, K, strides and alignment (the reference's vec8 row kernels need N a multiple
+ *   of 8 and N >= 2048, bgemm_test.cu:405-408). hk_bgemm routes its M == 1 and N == 1 products
+ *   here as well.
+ * ---------------------------------------------------------------------------------------- */
+HK_API hipError_t hk_bgemv_nn_row(int N, int K, hk_bf16 alpha, const hk_bf16* A, const hk_bf16* B,
+                                  int ldb, hk_bf16 beta, hk_bf16* C, int batchCount, long long sA,
+                                  long long sB, long long sC, hipStream_t stream);
+HK_API hipError_t hk_bgemv_nt_row(int N, int K, hk_bf16 alpha, const hk_bf16* A, const hk_bf16* B,
+                                  int ldb, hk_bf16 beta, hk_bf16* C, int batchCount, long long sA,
+                                  long long sB, long long sC, hipStream_t stream);
+HK_API hipError_t hk_bgemv_tn_row(int N, int K, hk_bf16 alpha, const hk_bf16* A, int lda,
+                                  const hk_bf16* B, int ldb, hk_bf16 beta, hk_bf16* C,
+                                  int batchCount, long long sA, long long sB, long long sC,
+                                  hipStream_t stream);
+HK_API hipError_t hk_bgemv_nn_col(int M, int K, hk_bf16 alpha, const hk_bf16* A, int lda,
+                                  const hk_bf16* B, hk_bf16 beta, hk_bf16* C, int batchCount,
+                                  long long sA, long long sB, long long sC, hipStream_t stream);
+
 /* BF16 GEMM with a bias, one semantics for both entry points:
  *   C = alpha * op(A) op(B) + beta * bias, C written and not read, the bias element of output
  *   (row, col) chosen by bias_numel: N -> bias[col], else M -> bias[row], else 1 -> bias[0],
