@@ -4,7 +4,9 @@
 // Reference behaviour:
 //   fused_attn_forward_kernel_tc_sm89<64, 64, 64, 1>
 //       kernels/attention/fused_attn_forward_kernel_tc_sm89.cu:72-426 (params :8-29):
-//       O = softmax(scale * Q K^T, key j <= query i when causal) V, LSE = max + ln(sum).
+//       O = softmax(scale * Q K^T, key j <= query i when causal) V, LSE = max + ln(sum);
+//       with dropout_p > 0 and a dropout_mask, the masked exp terms are normalised by their own
+//       sum (:316-334).
 //   mem_efficient_bwd_precompute_D_sm89<64>
 //       kernels/attention/mem_efficient_bwd_precompute_D_sm89.cu:45-91: D = rowsum(dO * O).
 //
@@ -21,6 +23,7 @@
 // global loads in flight. 35 KB of LDS and <= 168 VGPRs per workgroup let 3 workgroups share a
 // CU, so the BASELINE grid (768 workgroups) runs in one round on 256 CUs. Causal workgroups stop
 // at the diagonal; their order is described at snake_item.
+#include <initializer_list>
 #include <mutex>
 
 #include "hk_device.h"
@@ -108,7 +111,14 @@ __device__ __forceinline__ int snake_item(int L, int n, int P) {
   return r * P + (m - 1 - j);
 }
 
-__global__ __launch_bounds__(256, 3) void attn_fwd_kernel(hk_attn_fwd_params p, int nbh, int ncu) {
+// DROP: the reference's dropout path (fused_attn…:316-334): each exp term is multiplied by
+// dropout_mask[(bh*T + q)*T + key] before it enters the row sum, so O is normalised by the
+// post-dropout sum and a row with nothing kept gets O = 0 and LSE = -inf. mvec: mask rows are
+// 16-byte aligned (T % 4 == 0, aligned base), so four keys load at once.
+// The mask factors take 16 more VGPRs: the dropout form runs 2 workgroups per CU, not 3.
+template <bool DROP>
+__global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd_params p,
+                                                                     int nbh, int ncu, int mvec) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
 
   const int64_t T = p.T;
@@ -165,6 +175,25 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_kernel(hk_attn_fwd_params p, 
     const float* vt_st = k_st + kKFloats;
     // a wave whose queries all precede this tile has nothing to add (causal)
     if (!p.is_causal || k0 <= q0w + 31) {
+      // dropout factors of this lane's 16 scores, loaded first so the score MFMAs hide them
+      float4 mk[4];
+      if (DROP) {
+        const float* mrow = p.dropout_mask + (static_cast<int64_t>(bh) * T + q) * T;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int64_t key = k0 + 8 * g + 4 * hh;
+          if (q < T && mvec) {
+            mk[g] = key < T ? *reinterpret_cast<const float4*>(mrow + key)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+          } else {
+            const bool ok = q < T;
+            mk[g].x = ok && key + 0 < T ? mrow[key + 0] : 0.f;
+            mk[g].y = ok && key + 1 < T ? mrow[key + 1] : 0.f;
+            mk[g].z = ok && key + 2 < T ? mrow[key + 2] : 0.f;
+            mk[g].w = ok && key + 3 < T ? mrow[key + 3] : 0.f;
+          }
+        }
+      }
       f32x16_t s = f32x16_t{};
       const float* krow = k_st + c * kKPitch + 32 * hh;
       float4 kf[8];
@@ -204,7 +233,12 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_kernel(hk_attn_fwd_params p, 
       float ls = 0.f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float e = fast_exp2(s[i] - mref);
+        float e = fast_exp2(s[i] - mref);
+        if (DROP) {
+          const float4 f = mk[i >> 2];
+          const float d = (i & 3) == 0 ? f.x : (i & 3) == 1 ? f.y : (i & 3) == 2 ? f.z : f.w;
+          e = s[i] == -INFINITY ? 0.f : e * d;  // masked scores never read their factor
+        }
         s[i] = e;
         ls += e;
       }
@@ -298,8 +332,10 @@ extern "C" hipError_t hk_fused_attn_forward(const hk_attn_fwd_params* params, in
   HK_CHECK_ARG(head_dim == kHD);
   HK_CHECK_ARG(p.B >= 0 && p.nh >= 0 && p.T >= 0);
   if (p.B == 0 || p.nh == 0 || p.T == 0) return hipSuccess;
-  HK_CHECK_ARG(p.dropout_p == 0.0f);  // the dropout path is not provided by this build
   HK_CHECK_ARG(p.Q && p.K && p.V && p.O && p.LSE);
+  // the reference applies its mask only when both are given (fused_attn…:321)
+  const bool drop = p.dropout_p > 0.0f && p.dropout_mask != nullptr;
+  const int mvec = drop && p.T % 4 == 0 && hk::aligned16(p.dropout_mask) ? 1 : 0;
   HK_CHECK_ARG(rows_aligned(p.Q, p.q_strideB, p.q_strideH, p.q_strideM) &&
                rows_aligned(p.K, p.k_strideB, p.k_strideH, p.k_strideM) &&
                rows_aligned(p.V, p.v_strideB, p.v_strideH, p.v_strideM) &&
@@ -310,13 +346,17 @@ extern "C" hipError_t hk_fused_attn_forward(const hk_attn_fwd_params* params, in
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
-    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel),
-                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                               static_cast<int>(kLdsBytes));
+    for (const void* k : {reinterpret_cast<const void*>(&attn_fwd_kernel<false>),
+                          reinterpret_cast<const void*>(&attn_fwd_kernel<true>)}) {
+      const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               static_cast<int>(kLdsBytes));
+      if (e != hipSuccess) attr = e;
+    }
   });
   HK_RETURN_IF_ERROR(attr);
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3(static_cast<unsigned>(nqt * bh)), dim3(256),
-                     kLdsBytes, stream, p, static_cast<int>(bh), hk::device_cu_count());
+  hipLaunchKernelGGL(drop ? attn_fwd_kernel<true> : attn_fwd_kernel<false>,
+                     dim3(static_cast<unsigned>(nqt * bh)), dim3(256), kLdsBytes, stream, p,
+                     static_cast<int>(bh), hk::device_cu_count(), mvec);
   return hk::launch_status();
 }
 

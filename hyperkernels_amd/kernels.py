@@ -305,19 +305,30 @@ def _set_strides(params, prefix: str, t: torch.Tensor) -> None:
     setattr(params, f"{prefix}_strideM", t.stride(2))
 
 
-def fused_attn_forward(q, k, v, causal: bool, scale: float | None = None, o=None, lse=None):
-    """fused_attn_forward_kernel_tc_sm89<64,64,64,1>: returns (O, LSE)."""
+def fused_attn_forward(q, k, v, causal: bool, scale: float | None = None, o=None, lse=None,
+                       dropout_p: float = 0.0, dropout_mask=None):
+    """fused_attn_forward_kernel_tc_sm89<64,64,64,1>: returns (O, LSE).
+
+    With dropout_p > 0 and a dropout_mask (contiguous fp32 [B, nh, T, T], the factor of each
+    score, e.g. 0 or 1 / (1 - p)), the exp terms are multiplied by the mask and normalised by
+    their post-dropout sum, as the reference kernel does (fused_attn_forward...:316-334)."""
     for t in (q, k, v):
         if not t.is_cuda or t.dtype != torch.float32:
             raise ValueError("fused_attn_forward: fp32 device tensors")
     B, H, T, D = q.shape
+    if dropout_mask is not None and (
+            not dropout_mask.is_cuda or dropout_mask.dtype != torch.float32
+            or tuple(dropout_mask.shape) != (B, H, T, T) or not dropout_mask.is_contiguous()):
+        raise ValueError("fused_attn_forward: dropout_mask is a contiguous fp32 [B, nh, T, T] "
+                         "device tensor")
     scale = D ** -0.5 if scale is None else scale
     o = torch.empty_like(q) if o is None else o
     lse = torch.empty(B, H, T, device=q.device, dtype=torch.float32) if lse is None else lse
     p = AttnFwdParams()
     p.Q, p.K, p.V, p.O, p.LSE = (t.data_ptr() for t in (q, k, v, o, lse))
     p.B, p.nh, p.T, p.scale, p.is_causal = B, H, T, scale, bool(causal)
-    p.dropout_p, p.dropout_mask = 0.0, None
+    p.dropout_p = dropout_p
+    p.dropout_mask = None if dropout_mask is None else dropout_mask.data_ptr()
     for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
         _set_strides(p, name, t)
     p.lse_strideB, p.lse_strideH = lse.stride(0), lse.stride(1)

@@ -399,7 +399,10 @@ HK_API hipError_t hk_sgemm_layout(int layout, int M, int N, int K, float alpha, 
  *     mem_efficient_bwd_unified_kernel_exp12.cu:11-38, has the same layout).
  * hk_fused_attn_forward replaces fused_attn_forward_kernel_tc_sm89<64, 64, 64, 1> (:72-74):
  *   O = softmax(scale Q K^T [+ causal mask j <= i]) V, LSE = max + ln(sum of exp).
- *   dropout_p must be 0 (the dropout path, :321-323, is not provided).
+ *   With dropout_p > 0 and a non-NULL dropout_mask (fp32 [B*nh, T, T], contiguous, indexed
+ *   (bh*T + i)*T + j as the reference does, :316-323), every exp term is multiplied by its
+ *   mask value and the row sum is taken afterwards: O is normalised by the post-dropout sum
+ *   and LSE = max + ln(that sum), -inf for a row with nothing kept (O = 0 there) (:326-345).
  * hk_attn_bwd_precompute_D replaces mem_efficient_bwd_precompute_D_sm89<HeadDim> (:45-91):
  *   D = rowsum(dO * O); any head_dim in [1, 256] (the reference instantiates 16, 32, 48, 64,
  *   80, 96, 128, 160, 192 and 256, :93-102) and any O / dO strides (unit last-dim stride).

@@ -68,7 +68,8 @@ _SIGS = {
     "oracle_reduce_inner": (None, [_f32p, _f32p, _i64, _i64, _i64]),
     "oracle_reduce_outer": (None, [_f32p, _f32p, _i64, _i64, _i64, _i64, _i64]),
     "oracle_reduce_selftest_input": (None, [_f32p, _i64]),
-    "oracle_attn_forward": (None, [_f32p, _f32p, _f32p, _i, _i, _i, _i, _f, _i, _f32p, _f32p]),
+    "oracle_attn_forward": (None, [_f32p, _f32p, _f32p, _i, _i, _i, _i, _f, _i, _NullableF32,
+                                   _f32p, _f32p]),
     "oracle_attn_precompute_D": (None, [_f32p, _f32p, _f32p, _i64, _i]),
     "oracle_attn_backward": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i, _f,
                                     _i, _f32p, _f32p, _f32p, _f32p]),
@@ -262,12 +263,15 @@ def reduce_selftest_input(n):
     return out
 
 
-def attn_forward(q, k, v, scale, causal):
+def attn_forward(q, k, v, scale, causal, mask=None):
+    """O, LSE of softmax attention; `mask` ([B, H, T, T] fp32 or None) is the reference's
+    dropout mask, applied to the exp terms before the row sum."""
     q, k, v = _c(q), _c(k), _c(v)
     B, H, T, D = q.shape
     o = np.empty_like(q)
     lse = np.empty((B, H, T), np.float32)
-    lib().oracle_attn_forward(q, k, v, B, H, T, D, scale, int(bool(causal)), o, lse)
+    lib().oracle_attn_forward(q, k, v, B, H, T, D, scale, int(bool(causal)),
+                              None if mask is None else _c(mask).reshape(-1), o, lse)
     return o, lse
 
 

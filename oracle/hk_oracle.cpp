@@ -304,9 +304,13 @@ ORACLE_API void oracle_reduce_selftest_input(float* out, int64_t n) {
 // ---------------------------------------------------------------------------------------------
 // Attention (kernels_test.cu:68-139, 459-481). [B,H,T,Hd] contiguous; LSE/D [B,H,T].
 // ---------------------------------------------------------------------------------------------
+// With `mask` (a [B*H, T, T] fp32 dropout mask, or NULL) each exp term is multiplied by
+// mask[(bh*T + i)*T + j] and the row sum is taken after that product, so O is normalised by the
+// post-dropout sum and LSE = m + log(l) is -inf for a row with nothing kept: the reference
+// kernel's dropout path (fused_attn_forward_kernel_tc_sm89.cu:316-334, 421-425).
 ORACLE_API void oracle_attn_forward(const float* Q, const float* K, const float* V, int B, int H,
-                                    int T, int Hd, float scale, int causal, float* O,
-                                    float* LSE) {
+                                    int T, int Hd, float scale, int causal, const float* mask,
+                                    float* O, float* LSE) {
 #pragma omp parallel for collapse(2) schedule(dynamic)
   for (int bh = 0; bh < B * H; ++bh) {
     for (int i = 0; i < T; ++i) {
@@ -329,13 +333,14 @@ ORACLE_API void oracle_attn_forward(const float* Q, const float* K, const float*
         const float* vj = V + base + static_cast<int64_t>(j) * Hd;
         double d = 0;
         for (int k = 0; k < Hd; ++k) d += static_cast<double>(qi[k]) * kj[k];
-        const float e = std::exp(static_cast<float>(d * scale) - m);
+        float e = std::exp(static_cast<float>(d * scale) - m);
+        if (mask) e *= mask[(static_cast<int64_t>(bh) * T + i) * T + j];
         l += e;
         for (int k = 0; k < Hd; ++k) oacc[k] += static_cast<double>(e) * vj[k];
       }
       const double inv = (l > 0) ? 1.0 / l : 0.0;
       for (int k = 0; k < Hd; ++k) O[base + static_cast<int64_t>(i) * Hd + k] = static_cast<float>(oacc[k] * inv);
-      LSE[lbase + i] = static_cast<float>(m + std::log(l));
+      LSE[lbase + i] = (l > 0) ? static_cast<float>(m + std::log(l)) : -INFINITY;
     }
   }
 }

@@ -211,3 +211,79 @@ def test_attn_precompute_D_strided_rows(hk, orc):
     torch.cuda.synchronize()
     assert max_rel(Dt.cpu().numpy(), ref) <= 1e-5
 
+
+
+def _mask(orc, B, H, T, seed, p=0.3):
+    """A 0 / (1 / (1 - p)) dropout mask, fp32 [B, H, T, T], every row keeping key 0."""
+    keep = orc.rand_uniform(B * H * T * T, seed, 0.0, 1.0).reshape(B, H, T, T) >= p
+    keep[..., 0] = True
+    return (keep / np.float32(1.0 - p)).astype(np.float32)
+
+
+@pytest.mark.parametrize("T", [64, 200, 201])  # 201: rows not 16-byte aligned (scalar loads)
+@pytest.mark.parametrize("causal", [False, True])
+def test_attn_forward_dropout_mask(hk, orc, T, causal):
+    # the reference's dropout path (fused_attn...:316-334): masked exp terms, post-dropout sum
+    B, H, D = 2, 3, 64
+    say("attn fwd dropout", T, causal)
+    q, k, v = _qkv(orc, B, H, T, D, (31, 32, 33), normal=True)
+    mask = _mask(orc, B, H, T, 34)
+    o, lse = hk.fused_attn_forward(*(torch.from_numpy(a).to(DEV) for a in (q, k, v)), causal,
+                                   dropout_p=0.3, dropout_mask=torch.from_numpy(mask).to(DEV))
+    torch.cuda.synchronize()
+    ro, rl = orc.attn_forward(q, k, v, 0.125, causal, mask=mask)
+    assert max_rel(o.cpu().numpy(), ro) <= 2e-3
+    assert max_rel(lse.cpu().numpy(), rl) <= 2e-3
+    # not the pre-dropout normalisation: that result differs from the reference's here
+    r0, _ = orc.attn_forward(q, k, v, 0.125, causal)
+    assert max_rel(o.cpu().numpy(), r0) > 2e-2
+
+
+def test_attn_forward_dropout_off_cases(hk, orc):
+    # dropout_p > 0 without a mask, or a mask with dropout_p == 0: no dropout (fused_attn...:321)
+    B, H, T, D = 1, 2, 96, 64
+    say("attn fwd dropout off")
+    q, k, v = (torch.from_numpy(a).to(DEV) for a in _qkv(orc, B, H, T, D, (41, 42, 43)))
+    mask = torch.from_numpy(_mask(orc, B, H, T, 44)).to(DEV)
+    ref_o, ref_l = hk.fused_attn_forward(q, k, v, True)
+    for kw in ({"dropout_p": 0.5}, {"dropout_p": 0.0, "dropout_mask": mask}):
+        o, lse = hk.fused_attn_forward(q, k, v, True, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(o, ref_o) and torch.equal(lse, ref_l)
+
+
+def test_attn_forward_dropout_row_with_nothing_kept(hk, orc):
+    B, H, T, D = 1, 1, 70, 64
+    say("attn fwd dropout empty row")
+    q, k, v = _qkv(orc, B, H, T, D, (51, 52, 53))
+    mask = _mask(orc, B, H, T, 54)
+    mask[0, 0, 9, :] = 0.0
+    o, lse = hk.fused_attn_forward(*(torch.from_numpy(a).to(DEV) for a in (q, k, v)), False,
+                                   dropout_p=0.3, dropout_mask=torch.from_numpy(mask).to(DEV))
+    torch.cuda.synchronize()
+    o, lse = o.cpu().numpy(), lse.cpu().numpy()
+    assert (o[0, 0, 9] == 0).all() and lse[0, 0, 9] == -np.inf
+    ro, rl = orc.attn_forward(q, k, v, 0.125, False, mask=mask)
+    keep = np.ones(T, bool)
+    keep[9] = False
+    assert max_rel(o[0, 0, keep], ro[0, 0, keep]) <= 2e-3
+    assert max_rel(lse[0, 0, keep], rl[0, 0, keep]) <= 2e-3
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attn_forward_dropout_baseline_shape_sampled_heads(hk, orc, causal):
+    # BASELINE configs[2] shape with a p = 0.1 mask; two (batch, head) pairs checked in full
+    B, H, T, D = 8, 12, 1024, 64
+    say("attn fwd dropout baseline", causal)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(7)
+    q, k, v = (torch.randn(B, H, T, D, generator=g, device=DEV) for _ in range(3))
+    mask = (torch.rand(B, H, T, T, generator=g, device=DEV) >= 0.1).float() / 0.9
+    o, lse = hk.fused_attn_forward(q, k, v, causal, dropout_p=0.1, dropout_mask=mask)
+    torch.cuda.synchronize()
+    for b, h in ((0, 0), (7, 11)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        ro, rl = orc.attn_forward(*(t[sl].cpu().numpy() for t in (q, k, v)), 0.125, causal,
+                                  mask=mask[sl].cpu().numpy())
+        assert max_rel(o[sl].cpu().numpy(), ro) <= 2e-3
+        assert max_rel(lse[sl].cpu().numpy(), rl) <= 2e-3

@@ -307,6 +307,51 @@ def test_attention_vs_torch_sdpa(orc, causal):
         assert max_rel(got, ref.numpy()) < 1e-4
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_dropout_mask_vs_torch_sdpa(orc, causal):
+    # The reference's dropout path multiplies each exp term by mask[(bh*T + i)*T + j] and
+    # normalises by the post-dropout sum (fused_attn...:316-334). For a positive mask that is
+    # softmax attention with the additive bias log(mask); for a 0/c mask it is attention over
+    # the kept keys only, with LSE shifted by log(c). Both are checked against torch float64
+    # SDPA with an attn_mask, on a mask that is not symmetric (a transposed index fails).
+    B, H, T, D = 1, 2, 40, 64
+    q, k, v = (orc.rand_uniform(B * H * T * D, s).reshape(B, H, T, D) for s in (111, 112, 113))
+    scale = 1.0 / np.sqrt(D)
+    qt, kt, vt = (torch.from_numpy(a).double() for a in (q, k, v))
+    causal_inf = torch.zeros(T, T, dtype=torch.float64)
+    if causal:
+        causal_inf = causal_inf.masked_fill(torch.ones(T, T, dtype=torch.bool).triu(1), -np.inf)
+    s = (qt @ kt.transpose(-1, -2)) * float(scale) + causal_inf
+    # positive mask: additive log bias
+    pos = orc.rand_uniform(B * H * T * T, 114, 0.25, 2.0).reshape(B, H, T, T)
+    o, lse = orc.attn_forward(q, k, v, scale, causal, mask=pos)
+    bias = torch.from_numpy(np.log(pos.astype(np.float64))) + causal_inf
+    ot = F.scaled_dot_product_attention(qt, kt, vt, attn_mask=bias, scale=float(scale))
+    assert max_rel(o, ot.numpy()) < 1e-5
+    assert max_rel(lse, torch.logsumexp(s + torch.from_numpy(np.log(pos.astype(np.float64))),
+                                        -1).numpy()) < 1e-5
+    # 0 / c mask (c = 1 / (1 - p), p = 0.3): attention over the kept keys, LSE + log c
+    c = 1.0 / 0.7
+    keep = orc.rand_uniform(B * H * T * T, 115, 0.0, 1.0).reshape(B, H, T, T) >= 0.3
+    keep[..., 0] = True  # every row keeps key 0, so no row is empty here
+    mask = (keep * c).astype(np.float32)
+    o, lse = orc.attn_forward(q, k, v, scale, causal, mask=mask)
+    drop_inf = torch.from_numpy(np.where(keep, 0.0, -np.inf)) + causal_inf
+    ot = F.scaled_dot_product_attention(qt, kt, vt, attn_mask=drop_inf, scale=float(scale))
+    assert max_rel(o, ot.numpy()) < 1e-5
+    ref_lse = torch.logsumexp(s + drop_inf, -1).numpy() + np.log(np.float32(c))
+    assert max_rel(lse, ref_lse) < 1e-5
+    # an all-ones mask is no dropout at all
+    o1, l1 = orc.attn_forward(q, k, v, scale, causal, mask=np.ones((B, H, T, T), np.float32))
+    o0, l0 = orc.attn_forward(q, k, v, scale, causal)
+    np.testing.assert_array_equal(o1, o0)
+    np.testing.assert_array_equal(l1, l0)
+    # a row with nothing kept: O = 0 and LSE = -inf (fused_attn...:333, 345)
+    mask[0, 1, 5, :] = 0.0
+    o, lse = orc.attn_forward(q, k, v, scale, causal, mask=mask)
+    assert (o[0, 1, 5] == 0).all() and lse[0, 1, 5] == -np.inf
+
+
 # ---------------------------------------------------------------------------------------------
 # GEMM
 # ---------------------------------------------------------------------------------------------
