@@ -283,12 +283,12 @@ def attention_cases(g):
         tag = "causal" if causal else "noncausal"
         cases.append((f"attn_fwd_{tag}_8x12x1024x64",
                       lambda c=causal, o=o, lse=lse: hk.fused_attn_forward(q, k, v, c, o=o, lse=lse),
-                      W.attn_fwd_flop(B, H, T, D, causal), "fp32_matrix"))
+                      W.attn_fwd_flop(B, H, T, D, causal), "bf16x3"))
         mask = (torch.rand(B, H, T, T, generator=g, device=DEV) >= 0.1).float() / 0.9
         cases.append((f"attn_fwd_dropout_{tag}_8x12x1024x64",
                       lambda c=causal, o=o, lse=lse, mask=mask: hk.fused_attn_forward(
                           q, k, v, c, o=o, lse=lse, dropout_p=0.1, dropout_mask=mask),
-                      W.attn_fwd_flop(B, H, T, D, causal), "fp32_matrix"))
+                      W.attn_fwd_flop(B, H, T, D, causal), "bf16x3"))
         cases.append((f"attn_bwd_{tag}_8x12x1024x64",
                       lambda c=causal, lse=lse, Dt=Dt, dq=dq, dk=dk, dv=dv: hk.attn_backward(
                           q, k, v, do, lse, Dt, c, dq=dq, dk=dk, dv=dv),

@@ -11,18 +11,20 @@
 //       kernels/attention/mem_efficient_bwd_precompute_D_sm89.cu:45-91: D = rowsum(dO * O).
 //
 // Design (gfx950): one workgroup = 4 waves = 128 query rows of one (batch, head); a wave owns 32
-// queries. Products run on the fp32 MFMA v_mfma_f32_32x32x2_f32 (exact fp32 products; the
-// reference rounds operands to TF32). The score tile is formed transposed, S^T = K Q^T, so
-// each lane owns one query column: the online-softmax max is one 32-value register reduction
-// plus a single cross-half shuffle, the rescale factor is per lane, and the exponentiated
-// scores are already laid out as the B operand of the next product, O^T += V^T P^T, which
-// keeps O^T per lane as well (no LDS round trip of P, no cross-lane gathers of the rescale).
-// Q stays in registers (pre-scaled by scale * log2 e, so the softmax uses the hardware exp2); K
-// and V tiles of 32 keys go through two LDS stages, K as [key][d] and V transposed as [d][key]
-// (rows padded to 68 / 36 floats: conflict-free 16-byte fragment reads), with the next tile's
-// global loads in flight. 35 KB of LDS and <= 168 VGPRs per workgroup let 3 workgroups share a
-// CU, so the BASELINE grid (768 workgroups) runs in one round on 256 CUs. Causal workgroups stop
-// at the diagonal; their order is described at snake_item.
+// queries. gfx950 has no TF32 MFMA; the products run as a bf16x3 split on
+// v_mfma_f32_32x32x16_bf16: each fp32 operand x becomes hi + lo (two bf16) and a product is
+// ah bh + ah bl + al bh, three bf16 MFMA products accumulated in fp32. That is fp32-class
+// accuracy (relative error ~1e-5, measured O max-rel 5e-6 against the fp32 CPU reference) at
+// 16 / 3 the throughput of the fp32 MFMA (v_mfma_f32_32x32x2_f32); the reference itself rounds
+// its operands to TF32. The score tile is formed transposed, S^T = K Q^T, so each lane owns one
+// query column: the online-softmax max is one 16-value register reduction plus a single
+// cross-half shuffle and the exponentiated scores are already laid out as the B operand of the
+// next product, O^T += V^T P^T (no LDS round trip of P). Q stays in registers (pre-scaled by
+// scale * log2 e, so the softmax uses the hardware exp2, split once); each K / V tile of 32 keys
+// is split while it is staged into LDS (K as [key][d], V transposed as [d][key]), with the next
+// tile's global loads in flight. 34 KB of LDS and <= 168 VGPRs per workgroup let 3 workgroups
+// share a CU, so the BASELINE grid (768 workgroups) runs in one round on 256 CUs. Causal
+// workgroups stop at the diagonal; their order is described at snake_item.
 #include <initializer_list>
 #include <mutex>
 
@@ -39,65 +41,130 @@ static_assert(sizeof(hk_attn_bwd_params) == 328, "hk_attn_bwd_params layout");
 namespace {
 
 constexpr int kHD = 64;
-constexpr int kBQ = 128;                 // queries per workgroup (4 waves x 32)
-constexpr int kBKV = 32;                 // keys per K/V tile
-constexpr int kKPitch = kHD + 4;         // K tile [key][d] row pitch (floats)
-constexpr int kVPitch = kBKV + 4;        // V^T tile [d][key] row pitch (floats)
-constexpr int kKFloats = kBKV * kKPitch;
-constexpr int kVFloats = kHD * kVPitch;
-constexpr int kStageFloats = kKFloats + kVFloats;
-constexpr size_t kLdsBytes = 2 * kStageFloats * sizeof(float);  // two stages, 35,840 bytes
+constexpr int kBQ = 128;   // queries per workgroup (4 waves x 32)
+constexpr int kBKV = 32;   // keys per K/V tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
+// LDS stage: K hi / K lo as [key][64 d] bf16 (128-byte rows, 16-byte chunk c of row r stored
+// at chunk c ^ ((r >> 1) & 7)), then V^T hi / V^T lo as [d][32 keys] bf16 with a 72-byte row
+// pitch. Both layouts make the fragment reads below conflict-free across 16 consecutive lanes.
+constexpr int kKBytes = kBKV * 128;                 // 4096
+constexpr int kVtPitch = 72;                        // bytes per V^T row
+constexpr int kVtBytes = kHD * kVtPitch;            // 4608
+constexpr int kStageBytes = 2 * kKBytes + 2 * kVtBytes;  // 17408
+constexpr size_t kLdsBytes = 2 * kStageBytes;             // 34816, two stages
+
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef short bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // 2^x with the hardware exp2 (v_exp_f32, ~1 ulp). Arguments are scores minus a running max, so
 // they are <= 0; results below 2^-126 flush to zero, which only drops terms that are at most
 // 2^-126 of the row's largest one.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// K/V tile loader: 32 keys x 64 floats of each of K and V = 512 16-byte vectors per tensor;
-// thread t moves vectors t and t + 256 (key f / 16, d (f % 16) * 4). K is stored as it lies
-// ([key][d], pitch 68), V transposed ([d][key], pitch 36) so that the P V product reads four
-// consecutive keys of one d with one 16-byte LDS read.
+// ---- bf16x3 split ------------------------------------------------------------------------------
+// x = hi + lo with hi = bf16(x) and lo = bf16(x - hi), both rounded to nearest even: |x - hi - lo|
+// <= 2^-18 |x|. A product a b is then ah bh + ah bl + al bh (the dropped al bl is below 2^-16 of
+// it), three bf16 MFMA products that are exact in fp32. Two fp32 values per call, packed as
+// bf16 pairs (element 0 in the low half).
+// Returns {hi pair, lo pair}.
+__device__ __forceinline__ u32x2_t split2(float x0, float x1) {
+  const uint32_t hi = __builtin_bit_cast(uint32_t,
+                                         __builtin_convertvector(f32x2_t{x0, x1}, bf16x2_t));
+  const float r0 = x0 - __uint_as_float(hi << 16);
+  const float r1 = x1 - __uint_as_float(hi & 0xffff0000u);
+  return u32x2_t{hi, __builtin_bit_cast(uint32_t,
+                                        __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t))};
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// v_mfma_f32_32x32x16_bf16: A (32 x 16) lane l holds row l % 32, k = 8 (l / 32) .. + 7; B (16 x 32)
+// lane l holds column l % 32, same k; C element i of lane l is (row 8 (i / 4) + 4 (l / 32) + i % 4,
+// column l % 32).
+__device__ __forceinline__ f32x16_t mfma(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16_t mfma3(bf16x8_t ah, bf16x8_t al, bf16x8_t bh, bf16x8_t bl,
+                                          f32x16_t c) {
+  c = mfma(ah, bh, c);
+  c = mfma(ah, bl, c);
+  return mfma(al, bh, c);
+}
+
+// K/V tile staging: thread t owns key rows 2 (t / 16) and 2 (t / 16) + 1 at d = 4 (t % 16) .. + 3
+// of both K and V (four 16-byte global loads, coalesced 256 bytes per 16 threads). K is split and
+// written as it lies; V is split and written transposed, the two keys of a d packed in one 32-bit
+// store.
 struct KVLoader {
-  const float* k;
-  const float* v;
-  int64_t ks, vs;  // row strides (elements)
+  const float* k0p;  // this thread's first K row (key 2 (t / 16)) at its column
+  const float* v0p;
+  int64_t ks, vs;    // row strides (elements)
   int64_t T;
 
-  __device__ void load(int64_t k0, float4 (&rk)[2], float4 (&rv)[2]) const {
-    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+  __device__ KVLoader(const float* k, const float* v, int64_t ks_, int64_t vs_, int64_t T_)
+      : ks(ks_), vs(vs_), T(T_) {
+    const int pr = threadIdx.x >> 4, col = (threadIdx.x & 15) * 4;
+    k0p = k + 2 * pr * ks + col;
+    v0p = v + 2 * pr * vs + col;
+  }
+  // Rows at or past T (only in the last tile) read row T - 1, always in bounds, and are zeroed
+  // by value, so the loads stay unconditional 16-byte global loads.
+  __device__ void load(int64_t k0, f32x4_t (&rk)[2], f32x4_t (&rv)[2]) const {
+    const float* kp = k0p + k0 * ks;
+    const float* vp = v0p + k0 * vs;
+    if (k0 + kBKV <= T) {  // whole tile in range (uniform)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        rk[j] = *reinterpret_cast<const f32x4_t*>(kp + j * ks);
+        rv[j] = *reinterpret_cast<const f32x4_t*>(vp + j * vs);
+      }
+      return;
+    }
+    const int pr = threadIdx.x >> 4;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int f = threadIdx.x + 256 * j;
-      const int64_t row = k0 + (f >> 4);
-      const int col = (f & 15) * 4;
-      rk[j] = row < T ? *reinterpret_cast<const float4*>(k + row * ks + col) : zero;
-      rv[j] = row < T ? *reinterpret_cast<const float4*>(v + row * vs + col) : zero;
+      const int64_t row = k0 + 2 * pr + j;
+      const int64_t back = row < T ? 0 : row - (T - 1);  // rows to step back to T - 1
+      rk[j] = *reinterpret_cast<const f32x4_t*>(kp + (j - back) * ks);
+      rv[j] = *reinterpret_cast<const f32x4_t*>(vp + (j - back) * vs);
+      if (row >= T) rk[j] = rv[j] = f32x4_t{};
     }
   }
-  __device__ static void store(float* st, const float4 (&rk)[2], const float4 (&rv)[2]) {
-    float* sk = st;
-    float* svt = st + kKFloats;
+  __device__ static void store(char* st, const f32x4_t (&rk)[2], const f32x4_t (&rv)[2]) {
+    const int pr = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 4;
+    char* kh = st;
+    char* kl = st + kKBytes;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int f = threadIdx.x + 256 * j;
-      const int key = f >> 4, d = (f & 15) * 4;
-      *reinterpret_cast<float4*>(sk + key * kKPitch + d) = rk[j];
-      svt[(d + 0) * kVPitch + key] = rv[j].x;
-      svt[(d + 1) * kVPitch + key] = rv[j].y;
-      svt[(d + 2) * kVPitch + key] = rv[j].z;
-      svt[(d + 3) * kVPitch + key] = rv[j].w;
+      const int key = 2 * pr + j;
+      const u32x2_t s0 = split2(rk[j].x, rk[j].y), s1 = split2(rk[j].z, rk[j].w);
+      const u32x2_t h = {s0.x, s1.x}, l = {s0.y, s1.y};
+      const int chunk = (d0 >> 3) ^ ((key >> 1) & 7);
+      const int off = key * 128 + chunk * 16 + (d0 & 7) * 2;
+      *reinterpret_cast<u32x2_t*>(kh + off) = h;
+      *reinterpret_cast<u32x2_t*>(kl + off) = l;
+    }
+    char* vh = st + 2 * kKBytes;
+    char* vl = vh + kVtBytes;
+    const float a[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w};
+    const float c[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x2_t hl = split2(a[i], c[i]);  // keys 2 pr and 2 pr + 1 of d0 + i
+      const int off = (d0 + i) * kVtPitch + 4 * pr;
+      *reinterpret_cast<uint32_t*>(vh + off) = hl.x;
+      *reinterpret_cast<uint32_t*>(vl + off) = hl.y;
     }
   }
 };
 
-// Per 32-key tile and wave (32 queries): S^T = K Q^T is one 32 x 32 accumulator block (32 MFMAs
-// over d), P^T = exp2(S^T - m) stays in that block's registers, and O^T += V^T P^T is two
-// blocks (d halves) of 16 MFMAs each. Accumulator element i of a lane (query c = lane % 32,
-// half hh = lane / 32) covers key 8 (i / 4) + 4 hh + i % 4 of the tile.
 // Work order. Workgroup L of the 1-D grid gets item snake(L): with P = number of CUs, round
 // r = L / P is traversed forwards for even r and backwards for odd r (a boustrophedon). Items
 // are numbered heaviest first (under causal masking q-tile nqt-1 of every (batch, head) first,
@@ -111,15 +178,23 @@ __device__ __forceinline__ int snake_item(int L, int n, int P) {
   return r * P + (m - 1 - j);
 }
 
+// Per 32-key tile and wave (32 queries):
+//   S^T = K Q^T: one 32 x 32 accumulator block, 4 k-steps of 16 d, 3 MFMAs each (bf16x3);
+//   P^T = exp2(S^T - m) stays in that block: lane (q = l % 32, h = l / 32) holds keys
+//     8 (i / 4) + 4 h + i % 4, i = 0..15;
+//   O^T += V^T P^T: two 32 x 32 blocks (d halves), 2 k-steps of 16 keys, 3 MFMAs each.
+// The P V product sums over keys in any order, so its k index runs over the keys in the order
+// the lane already holds them: k-step s, k = 8 h + j is key 16 s + 4 h + j (j < 4) or
+// 16 s + 8 + 4 h + (j - 4). The B operand of k-step s is then P elements 8 s .. 8 s + 7 as they
+// are, and the V^T fragment is two 8-byte reads at those key offsets.
 // DROP: the reference's dropout path (fused_attn…:316-334): each exp term is multiplied by
 // dropout_mask[(bh*T + q)*T + key] before it enters the row sum, so O is normalised by the
 // post-dropout sum and a row with nothing kept gets O = 0 and LSE = -inf. mvec: mask rows are
 // 16-byte aligned (T % 4 == 0, aligned base), so four keys load at once.
-// The mask factors take 16 more VGPRs: the dropout form runs 2 workgroups per CU, not 3.
 template <bool DROP>
 __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd_params p,
                                                                      int nbh, int ncu, int mvec) {
-  extern __shared__ __attribute__((aligned(16))) float lds[];
+  extern __shared__ __attribute__((aligned(16))) char lds[];
 
   const int64_t T = p.T;
   const int nqt = static_cast<int>((T + kBQ - 1) / kBQ);
@@ -137,18 +212,21 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
   const int64_t q0w = static_cast<int64_t>(qt) * kBQ + wave * 32;
   const int64_t q = q0w + c;
 
-  // Q row (this lane's half of the head dim), scaled so that scores are in log2 units.
-  float qr[32];
+  // Q^T operands (B of S^T = K Q^T): k-step s holds d = 16 s + 8 hh .. + 7 of query q, scaled so
+  // that scores are in log2 units, split into bf16 hi / lo.
+  bf16x8_t qh[4], ql[4];
   {
     const float qs = p.scale * kLog2e;
-    const float* qp = Qb + q * p.q_strideM + 32 * hh;
+    const float* qp = Qb + (q < T ? q : T - 1) * p.q_strideM + 8 * hh;  // row T-1: in bounds
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float4 v = q < T ? *reinterpret_cast<const float4*>(qp + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
-      qr[4 * j + 0] = v.x * qs;
-      qr[4 * j + 1] = v.y * qs;
-      qr[4 * j + 2] = v.z * qs;
-      qr[4 * j + 3] = v.w * qs;
+    for (int s = 0; s < 4; ++s) {
+      f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(qp + 16 * s);
+      f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(qp + 16 * s + 4);
+      if (q >= T) v0 = v1 = f32x4_t{};
+      const u32x2_t a0 = split2(v0.x * qs, v0.y * qs), a1 = split2(v0.z * qs, v0.w * qs);
+      const u32x2_t a2 = split2(v1.x * qs, v1.y * qs), a3 = split2(v1.z * qs, v1.w * qs);
+      qh[s] = as_bf16x8(u32x4_t{a0.x, a1.x, a2.x, a3.x});
+      ql[s] = as_bf16x8(u32x4_t{a0.y, a1.y, a2.y, a3.y});
     }
   }
 
@@ -157,107 +235,150 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
 
   const int64_t kv_end = p.is_causal ? (static_cast<int64_t>(qt) * kBQ + kBQ < T ? static_cast<int64_t>(qt) * kBQ + kBQ : T) : T;
   const int nkv = static_cast<int>((kv_end + kBKV - 1) / kBKV);
-  KVLoader ld{p.K + b * p.k_strideB + h * p.k_strideH, p.V + b * p.v_strideB + h * p.v_strideH,
-              p.k_strideM, p.v_strideM, T};
-  float4 rk[2], rv[2];
+  const KVLoader ld(p.K + b * p.k_strideB + h * p.k_strideH,
+                    p.V + b * p.v_strideB + h * p.v_strideH, p.k_strideM, p.v_strideM, T);
+  f32x4_t rk[2], rv[2];
+  // per-lane LDS offsets: K fragment (key c, chunk 2 s + hh), V^T fragments (row 32 db + c)
+  const int kswz = (c >> 1) & 7;
+  const int vt_row = c * kVtPitch + 8 * hh;
+  // a wave whose queries all precede key tile kt has nothing to add there (causal)
+  auto active = [&](int kt) {
+    return !p.is_causal || static_cast<int64_t>(kt) * kBKV <= q0w + 31;
+  };
+  // Scores of a tile relative to the running reference m: the accumulator starts at -m (0
+  // while this query has no reference yet), so the MFMAs deliver s - m directly.
+  auto base_of = [&](float mm) { return mm == -INFINITY ? 0.f : -mm; };
+  auto qk = [&](const char* st, float c0) {
+    f32x16_t sc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sc[i] = c0;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int off = c * 128 + (((2 * ks + hh) ^ kswz) * 16);
+      const bf16x8_t kh = as_bf16x8(*reinterpret_cast<const u32x4_t*>(st + off));
+      const bf16x8_t kl = as_bf16x8(*reinterpret_cast<const u32x4_t*>(st + kKBytes + off));
+      sc = mfma3(kh, kl, qh[ks], ql[ks], sc);
+    }
+    return sc;
+  };
+
+  // Online softmax with a lazily moved reference (log2 units): m changes only when a tile's
+  // scores exceed it by more than kTau or on the query's first tile, so exp2(s - m) <= 2^kTau
+  // and most tiles need neither a subtraction per score nor a rescale of O.
+  constexpr float kTau = 8.f;
+  auto softmax_pv = [&](int kt, f32x16_t& sc, float c0, const char* st) {
+    const int64_t k0 = static_cast<int64_t>(kt) * kBKV;
+    // scores formed against an older reference are moved onto the current one
+    const float cnow = base_of(m);
+    if (__builtin_amdgcn_ballot_w64(c0 != cnow) != 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sc[i] += cnow - c0;
+    }
+    // dropout factors of this lane's 16 scores
+    float4 mk[4];
+    if (DROP) {
+      const float* mrow = p.dropout_mask + (static_cast<int64_t>(bh) * T + q) * T;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t key = k0 + 8 * g + 4 * hh;
+        if (q < T && mvec) {
+          mk[g] = key < T ? *reinterpret_cast<const float4*>(mrow + key)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+          const bool ok = q < T;
+          mk[g].x = ok && key + 0 < T ? mrow[key + 0] : 0.f;
+          mk[g].y = ok && key + 1 < T ? mrow[key + 1] : 0.f;
+          mk[g].z = ok && key + 2 < T ? mrow[key + 2] : 0.f;
+          mk[g].w = ok && key + 3 < T ? mrow[key + 3] : 0.f;
+        }
+      }
+    }
+    // mask (causal: key > query; any: key >= T)
+    const bool need_mask = (p.is_causal && k0 + kBKV - 1 > q0w) || k0 + kBKV > T;
+    if (need_mask) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t key = k0 + 8 * (i >> 2) + 4 * hh + (i & 3);
+        if (key >= T || (p.is_causal && key > q)) sc[i] = -INFINITY;
+      }
+    }
+    float mt = sc[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mt = fmaxf(mt, sc[i]);
+    mt = fmaxf(mt, __shfl_xor(mt, 32, HK_WAVE));
+    // The reference moves on the query's first tile with an unmasked score, and when a score
+    // exceeds it by more than kTau; otherwise (most tiles) it stays.
+    const bool first = m == -INFINITY;
+    const bool move = mt != -INFINITY && (first || mt > kTau);
+    if (__builtin_amdgcn_ballot_w64(move) != 0) {
+      const float shift = move ? mt : 0.f;
+      const float alpha = move && !first ? fast_exp2(-shift) : 1.f;
+      if (move) m = first ? shift : m + shift;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sc[i] -= shift;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 2; ++db) o[db] *= alpha;
+    }
+    float ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float e = fast_exp2(sc[i]);
+      if (DROP) {
+        const float4 f = mk[i >> 2];
+        const float dm = (i & 3) == 0 ? f.x : (i & 3) == 1 ? f.y : (i & 3) == 2 ? f.z : f.w;
+        e = sc[i] == -INFINITY ? 0.f : e * dm;  // masked scores never read their factor
+      }
+      sc[i] = e;
+      ls += e;
+    }
+    l += ls;
+    // P^T operands (B of O^T += V^T P^T): k-step ks = elements 8 ks .. 8 ks + 7, split
+    bf16x8_t ph[2], pl[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const u32x2_t a0 = split2(sc[8 * ks + 0], sc[8 * ks + 1]);
+      const u32x2_t a1 = split2(sc[8 * ks + 2], sc[8 * ks + 3]);
+      const u32x2_t a2 = split2(sc[8 * ks + 4], sc[8 * ks + 5]);
+      const u32x2_t a3 = split2(sc[8 * ks + 6], sc[8 * ks + 7]);
+      ph[ks] = as_bf16x8(u32x4_t{a0.x, a1.x, a2.x, a3.x});
+      pl[ks] = as_bf16x8(u32x4_t{a0.y, a1.y, a2.y, a3.y});
+    }
+    const char* vh = st + 2 * kKBytes;
+    const char* vl = vh + kVtBytes;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        // keys 16 ks + 4 hh .. + 3 and 16 ks + 8 + 4 hh .. + 3 of row d = 32 db + c
+        const int off = vt_row + 32 * db * kVtPitch + 32 * ks;
+        const u32x2_t a0 = *reinterpret_cast<const u32x2_t*>(vh + off);
+        const u32x2_t a1 = *reinterpret_cast<const u32x2_t*>(vh + off + 16);
+        const u32x2_t b0 = *reinterpret_cast<const u32x2_t*>(vl + off);
+        const u32x2_t b1 = *reinterpret_cast<const u32x2_t*>(vl + off + 16);
+        o[db] = mfma3(as_bf16x8(u32x4_t{a0.x, a0.y, a1.x, a1.y}),
+                      as_bf16x8(u32x4_t{b0.x, b0.y, b1.x, b1.y}), ph[ks], pl[ks], o[db]);
+      }
+  };
+
+  // Two LDS stages: step kt forms and finishes tile kt from one stage while the global loads
+  // of tile kt + 1 are in flight; they land in the other stage at the end of the step.
   if (nkv > 0) {
     ld.load(0, rk, rv);
     KVLoader::store(lds, rk, rv);
   }
   __syncthreads();
-
   for (int kt = 0; kt < nkv; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < nkv;
     if (more) ld.load(static_cast<int64_t>(kt + 1) * kBKV, rk, rv);
-    const int64_t k0 = static_cast<int64_t>(kt) * kBKV;
-    const float* k_st = lds + cur * kStageFloats;
-    const float* vt_st = k_st + kKFloats;
-    // a wave whose queries all precede this tile has nothing to add (causal)
-    if (!p.is_causal || k0 <= q0w + 31) {
-      // dropout factors of this lane's 16 scores, loaded first so the score MFMAs hide them
-      float4 mk[4];
-      if (DROP) {
-        const float* mrow = p.dropout_mask + (static_cast<int64_t>(bh) * T + q) * T;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int64_t key = k0 + 8 * g + 4 * hh;
-          if (q < T && mvec) {
-            mk[g] = key < T ? *reinterpret_cast<const float4*>(mrow + key)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-          } else {
-            const bool ok = q < T;
-            mk[g].x = ok && key + 0 < T ? mrow[key + 0] : 0.f;
-            mk[g].y = ok && key + 1 < T ? mrow[key + 1] : 0.f;
-            mk[g].z = ok && key + 2 < T ? mrow[key + 2] : 0.f;
-            mk[g].w = ok && key + 3 < T ? mrow[key + 3] : 0.f;
-          }
-        }
-      }
-      f32x16_t s = f32x16_t{};
-      const float* krow = k_st + c * kKPitch + 32 * hh;
-      float4 kf[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) kf[j] = *reinterpret_cast<const float4*>(krow + 4 * j);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].x, qr[4 * j + 0], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].y, qr[4 * j + 1], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].z, qr[4 * j + 2], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].w, qr[4 * j + 3], s, 0, 0, 0);
-      }
-      // V^T operands of this tile: row d = 32 db + c, keys 8 g + 4 hh .. +3
-      float4 vf[2][4];
-#pragma unroll
-      for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          vf[db][g] = *reinterpret_cast<const float4*>(vt_st + (32 * db + c) * kVPitch + 8 * g + 4 * hh);
-      // mask (causal: key > query; any: key >= T), tile max over this query's 32 keys
-      const bool need_mask = (p.is_causal && k0 + kBKV - 1 > q0w) || k0 + kBKV > T;
-      if (need_mask) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int64_t key = k0 + 8 * (i >> 2) + 4 * hh + (i & 3);
-          if (key >= T || (p.is_causal && key > q)) s[i] = -INFINITY;
-        }
-      }
-      float mt = s[0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) mt = fmaxf(mt, s[i]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32, HK_WAVE));
-      const float m_new = fmaxf(m, mt);
-      // rows with nothing unmasked so far keep m = -inf and contribute nothing
-      const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m - m_new);
-      const float mref = (m_new == -INFINITY) ? 0.f : m_new;
-      float ls = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float e = fast_exp2(s[i] - mref);
-        if (DROP) {
-          const float4 f = mk[i >> 2];
-          const float d = (i & 3) == 0 ? f.x : (i & 3) == 1 ? f.y : (i & 3) == 2 ? f.z : f.w;
-          e = s[i] == -INFINITY ? 0.f : e * d;  // masked scores never read their factor
-        }
-        s[i] = e;
-        ls += e;
-      }
-      l = l * alpha + ls;
-      m = m_new;
-#pragma unroll
-      for (int db = 0; db < 2; ++db) o[db] *= alpha;
-      // O^T[d][q] += sum_key V^T[d][key] P^T[key][q]
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[db][g].x, s[4 * g + 0], o[db], 0, 0, 0);
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[db][g].y, s[4 * g + 1], o[db], 0, 0, 0);
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[db][g].z, s[4 * g + 2], o[db], 0, 0, 0);
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[db][g].w, s[4 * g + 3], o[db], 0, 0, 0);
-        }
+    const char* st = lds + cur * kStageBytes;
+    if (active(kt)) {
+      const float c0 = base_of(m);
+      f32x16_t sc = qk(st, c0);
+      softmax_pv(kt, sc, c0, st);
     }
-    if (more) KVLoader::store(lds + (cur ^ 1) * kStageFloats, rk, rv);
+    if (more) KVLoader::store(lds + (cur ^ 1) * kStageBytes, rk, rv);
     __syncthreads();
   }
 

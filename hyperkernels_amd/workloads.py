@@ -85,4 +85,6 @@ def gemm_flop(M, N, K, batch=1):
 
 # MI355X published peaks (AMD): HBM3E bandwidth and dense matrix throughput.
 PEAK_HBM_GBS = 8000.0
-PEAK_TFLOPS = {"bf16": 2516.6, "fp32_matrix": 157.3}
+PEAK_TFLOPS = {"bf16": 2516.6, "fp32_matrix": 157.3,
+               # fp32 products computed as a bf16x3 split: three bf16 MFMA products each
+               "bf16x3": 2516.6 / 3}
