@@ -292,7 +292,7 @@ def attention_cases(g):
         cases.append((f"attn_bwd_{tag}_8x12x1024x64",
                       lambda c=causal, lse=lse, Dt=Dt, dq=dq, dk=dk, dv=dv: hk.attn_backward(
                           q, k, v, do, lse, Dt, c, dq=dq, dk=dk, dv=dv),
-                      W.attn_bwd_flop(B, H, T, D, causal), "fp32_matrix"))
+                      W.attn_bwd_flop(B, H, T, D, causal), "bf16x3"))
     return cases
 
 

@@ -8,18 +8,23 @@
 //
 // Design (gfx950): one workgroup = 8 waves owns 128 keys of one (batch, head): wave w takes key
 // group w % 4 (32 keys) and query half w / 4 of every 64-query tile, so each SIMD runs two
-// waves (latency of one hidden behind the other's MFMAs). K and V of the tile are loaded to
-// LDS once; query tiles (Q, dO, LSE, D) stream through LDS with the next tile's global loads
-// in flight. Per query tile a wave runs, on the fp32 MFMA v_mfma_f32_32x32x2_f32 (exact fp32
-// products): S = Q K^T and dP = dO V^T for its 32 x 32 block (accumulators hold one key column
+// waves. gfx950 has no TF32 MFMA; every product runs as a bf16x3 split on
+// v_mfma_f32_32x32x16_bf16 (x = hi + lo in bf16, a b = ah bh + ah bl + al bh accumulated in
+// fp32, relative error ~1e-5). K and V of the tile are split and staged into LDS once; query
+// tiles (Q, dO, LSE, D) are split and stream through LDS with the next tile's global loads in
+// flight. All LDS operands are bf16 hi / lo pairs of [rows][64] arrays (128-byte rows) read two
+// ways: 16-byte reads for a contraction over the head dimension, and the gfx950 transposing read
+// ds_read_b64_tr_b16 for a contraction over rows, so each tensor is stored once. Per query tile
+// a wave forms S = Q K^T and dP = dO V^T for its 32 x 32 block (accumulators hold one key column
 // per lane), P and dS in registers, then its query half's share of dV += P^T dO and
-// dK += dS^T Q straight from those accumulators (their register order is the MFMA operand
-// order for a contraction over queries). dS goes through LDS once so that dQ = dS K is formed
-// per (query block, d block, key half) with lanes along the head dimension; the two key halves
-// are summed through LDS and each dQ element receives one atomic add per key tile. The two
-// query halves' dK / dV partials are summed through LDS at the end. 128-key tiles mean 8 dQ
-// passes per query row at T = 1024 (the reference's 16-key tiles make 64). Workgroups are
-// ordered key tile major, so under causal masking the longest ones are dispatched first.
+// dK += dS^T Q with P / dS as the register operand (the contraction over queries runs in the
+// order the lane holds them; the dO / Q operand is read in the same order). dS^T goes through
+// LDS once so that dQ = dS K is formed per (query block, d block, key half) with lanes along the
+// head dimension; the two key halves are summed through LDS and each dQ element receives one
+// atomic add per key tile. The two query halves' dK / dV partials are summed through LDS at the
+// end. 128-key tiles mean 8 dQ passes per query row at T = 1024 (the reference's 16-key tiles
+// make 64). Workgroups are ordered key tile major, so under causal masking the longest ones are
+// dispatched first.
 #include <mutex>
 
 #include "hk_device.h"
@@ -28,67 +33,152 @@
 namespace {
 
 constexpr int kHD = 64;
-constexpr int kBKV = 128;                 // keys per workgroup
-constexpr int kBQ = 64;                   // queries per inner tile
-constexpr int kThreads = 512;             // 8 waves: 4 key groups x 2 query halves
-constexpr int kPitch = kHD + 4;           // LDS pitch for [rows][64] tiles (floats)
-constexpr int kSPitch = kBKV + 4;         // LDS pitch for the dS tile [64 q][128 keys]
-constexpr int kOffK = 0;
-constexpr int kOffV = kOffK + kBKV * kPitch;
-constexpr int kOffQ = kOffV + kBKV * kPitch;
-constexpr int kOffdO = kOffQ + kBQ * kPitch;
-constexpr int kOffdS = kOffdO + kBQ * kPitch;
-constexpr int kOffL = kOffdS + kBQ * kSPitch;
-constexpr int kOffD = kOffL + kBQ;
-constexpr int kLdsFloats = kOffD + kBQ;
-constexpr size_t kLdsBytes = kLdsFloats * sizeof(float);  // 142,336 bytes
+constexpr int kBKV = 128;        // keys per workgroup
+constexpr int kBQ = 64;          // queries per inner tile
+constexpr int kThreads = 512;    // 8 waves: 4 key groups x 2 query halves
 constexpr float kLog2e = 1.4426950408889634f;
 
+// LDS (bytes). Every [rows][64] bf16 array has 128-byte rows whose 16-byte chunk c of row r sits
+// at chunk c ^ swz(r); each has a hi and a lo plane.
+constexpr int kRowBytes = 128;
+constexpr int kKPlane = kBKV * kRowBytes;  // 16 KiB
+constexpr int kQPlane = kBQ * kRowBytes;   // 8 KiB
+constexpr int kOffKh = 0, kOffKl = kOffKh + kKPlane;
+constexpr int kOffVh = kOffKl + kKPlane, kOffVl = kOffVh + kKPlane;
+constexpr int kOffQh = kOffVl + kKPlane, kOffQl = kOffQh + kQPlane;
+constexpr int kOffOh = kOffQl + kQPlane, kOffOl = kOffOh + kQPlane;  // dO
+constexpr int kOffSh = kOffOl + kQPlane, kOffSl = kOffSh + kKPlane;  // dS^T [key][query]
+constexpr int kOffL = kOffSl + kKPlane;
+constexpr int kOffD = kOffL + kBQ * 4;
+constexpr size_t kLdsBytes = kOffD + kBQ * 4;  // 131,584 bytes
+// The dQ key-half exchange reuses the Q / dO planes (4 blocks of 32 x 33 floats); the final
+// dK / dV exchange reuses the start of LDS (4 key groups x 2 x 32 x 65 floats).
+static_assert(4 * 32 * 33 * 4 <= 4 * kQPlane, "dQ exchange fits the Q / dO planes");
+static_assert(4 * 2 * 32 * 65 * 4 <= kLdsBytes, "dK / dV exchange fits");
+
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef short bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ f32x16_t mfma(float a, float b, f32x16_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+#define HK_LDS __attribute__((address_space(3)))
+
+// Chunk permutation of row r. 16 consecutive rows at one logical chunk (a 16-byte operand read)
+// and 4 consecutive rows x 4 consecutive chunks (a transposing read of 32 lanes) both land on
+// distinct banks.
+__device__ __forceinline__ int swz(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
+__device__ __forceinline__ int off128(int r, int chunk) { return r * kRowBytes + ((chunk ^ swz(r)) << 4); }
+
+// x = hi + lo, both bf16 rounded to nearest even (|x - hi - lo| <= 2^-18 |x|); returns the
+// {hi pair, lo pair} of two values, element 0 in the low half.
+__device__ __forceinline__ u32x2_t split2(float x0, float x1) {
+  const uint32_t hi = __builtin_bit_cast(uint32_t,
+                                         __builtin_convertvector(f32x2_t{x0, x1}, bf16x2_t));
+  const float r0 = x0 - __uint_as_float(hi << 16);
+  const float r1 = x1 - __uint_as_float(hi & 0xffff0000u);
+  return u32x2_t{hi, __builtin_bit_cast(uint32_t,
+                                        __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t))};
+}
+// Eight values -> {hi x8, lo x8}.
+__device__ __forceinline__ void split8(const float* x, u32x4_t& hi, u32x4_t& lo) {
+  const u32x2_t a = split2(x[0], x[1]), b = split2(x[2], x[3]);
+  const u32x2_t c = split2(x[4], x[5]), d = split2(x[6], x[7]);
+  hi = u32x4_t{a.x, b.x, c.x, d.x};
+  lo = u32x4_t{a.y, b.y, c.y, d.y};
 }
 
-// Loads rows [r0, r0 + n) x 64 floats of a strided [T][64] tensor: 16 lanes per 256-byte row;
-// thread t moves vectors t + 512 j. Rows at or beyond T read as zero.
-template <int NV>
-__device__ __forceinline__ void load_rows(const float* base, int64_t stride, int64_t r0,
-                                          int64_t T, float4 (&reg)[NV]) {
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// v_mfma_f32_32x32x16_bf16: A (32 x 16) lane l holds row l % 32, k = 8 (l / 32) .. + 7; B (16 x 32)
+// lane l holds column l % 32, same k; C element i of lane l is (row 8 (i / 4) + 4 (l / 32) + i % 4,
+// column l % 32).
+__device__ __forceinline__ f32x16_t mfma3(bf16x8_t ah, bf16x8_t al, bf16x8_t bh, bf16x8_t bl,
+                                          f32x16_t c) {
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, c, 0, 0, 0);
+}
+
+// Operand of 8 consecutive head-dim elements (chunk `chunk`) of row `row`: one 16-byte read.
+__device__ __forceinline__ bf16x8_t rd_row(const char HK_LDS* plane, int row, int chunk) {
+  return *reinterpret_cast<const bf16x8_t HK_LDS*>(plane + off128(row, chunk));
+}
+
+// Transposed operand: the contraction runs over rows. Lane l gets column c0 + l % 32 and rows
+// r0 .. r0 + 3 (elements 0-3) and r1 .. r1 + 3 (elements 4-7), where r0 and r1 may depend on
+// l / 32 and are multiples of 4. ds_read_b64_tr_b16: within each 16-lane group, lane j reads
+// 4 bf16 of row rb + j / 4 at columns cb + 4 (j % 4), and lane i of the group receives column
+// cb + i of rows rb .. rb + 3.
+__device__ __forceinline__ bf16x8_t rd_tr(const char HK_LDS* plane, int c0, int r0, int r1,
+                                          int lane) {
+  const int j = lane & 15;
+  const int col = c0 + 16 * ((lane >> 4) & 1) + 4 * (j & 3);
+  const int ra = r0 + (j >> 2), rb = r1 + (j >> 2);
+  const bf16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (bf16x4_t HK_LDS*)(plane + off128(ra, col >> 3) + (col & 7) * 2));
+  const bf16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (bf16x4_t HK_LDS*)(plane + off128(rb, col >> 3) + (col & 7) * 2));
+  return bf16x8_t{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Stages rows [r0, r0 + ROWS) x 64 floats of a strided tensor into a hi / lo plane pair:
+// thread t handles row t / TPR, TPR threads per row, 64 / TPR floats (whole 16-byte chunks)
+// each. Rows at or past T are zero. `reg` holds the fp32 values between load and store so that
+// the global loads of the next tile can be in flight during the current one.
+template <int ROWS>
+struct Stager {
+  static constexpr int kTPR = kThreads / ROWS;     // threads per row: 8 (Q, dO) or 4 (K, V)
+  static constexpr int kFloats = kHD / kTPR;       // 8 or 16
+  static constexpr int kVec = kFloats / 4;
+  f32x4_t reg[kVec];
+  __device__ void load(const float* base, int64_t stride, int64_t r0, int64_t T) {
+    const int64_t row = r0 + threadIdx.x / kTPR;
+    const int col = (threadIdx.x % kTPR) * kFloats;
+    const int64_t rr = row < T ? row : T - 1;  // in bounds; zeroed below
+    const float* src = base + rr * stride + col;
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int f = threadIdx.x + kThreads * j;
-    const int64_t row = r0 + (f >> 4);
-    reg[j] = row < T ? *reinterpret_cast<const float4*>(base + row * stride + (f & 15) * 4)
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-}
-
-template <int NV>
-__device__ __forceinline__ void store_rows(float* lds, const float4 (&reg)[NV]) {
+    for (int v = 0; v < kVec; ++v) reg[v] = *reinterpret_cast<const f32x4_t*>(src + 4 * v);
+    if (row >= T) {
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int f = threadIdx.x + kThreads * j;
-    *reinterpret_cast<float4*>(lds + (f >> 4) * kPitch + (f & 15) * 4) = reg[j];
+      for (int v = 0; v < kVec; ++v) reg[v] = f32x4_t{};
+    }
   }
-}
+  __device__ void store(char HK_LDS* hi, char HK_LDS* lo) const {
+    const int row = threadIdx.x / kTPR;
+    const int chunk0 = (threadIdx.x % kTPR) * (kFloats / 8);
+#pragma unroll
+    for (int cc = 0; cc < kFloats / 8; ++cc) {
+      const float x[8] = {reg[2 * cc][0], reg[2 * cc][1], reg[2 * cc][2], reg[2 * cc][3],
+                          reg[2 * cc + 1][0], reg[2 * cc + 1][1], reg[2 * cc + 1][2],
+                          reg[2 * cc + 1][3]};
+      u32x4_t h, l;
+      split8(x, h, l);
+      const int off = off128(row, chunk0 + cc);
+      *reinterpret_cast<u32x4_t HK_LDS*>(hi + off) = h;
+      *reinterpret_cast<u32x4_t HK_LDS*>(lo + off) = l;
+    }
+  }
+};
 
-// Wave w owns key group kg = w % 4 (32 keys) and query half qh = w / 4 (32 of the tile's 64
-// queries). Per query tile it forms S and dP for its 32 x 32 block (lane (c, hh) holds key
-// column c, queries 8 (i/4) + 4 hh + i%4), turns them into P and dS in registers, and adds its
-// query half's share of dV = P^T dO and dK = dS^T Q for its keys. dS goes to LDS; dQ = dS K is
-// then split as 4 (query block, d block) pairs x 2 key halves over the 8 waves, the two key
-// halves are summed through LDS and one atomic add per dQ element and key tile goes to HBM.
-// At the end the two query halves' dK / dV partials of each key group are summed through LDS.
 __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_params p, int nbh) {
-  extern __shared__ __attribute__((aligned(16))) float lds[];
-  float* sK = lds + kOffK;
-  float* sV = lds + kOffV;
-  float* sQ = lds + kOffQ;
-  float* sdO = lds + kOffdO;
-  float* sdS = lds + kOffdS;
-  float* sL = lds + kOffL;
-  float* sD = lds + kOffD;
+  extern __shared__ __attribute__((aligned(16))) char lds_generic[];
+  char HK_LDS* lds = (char HK_LDS*)lds_generic;
+  char HK_LDS* sKh = lds + kOffKh;
+  char HK_LDS* sKl = lds + kOffKl;
+  char HK_LDS* sVh = lds + kOffVh;
+  char HK_LDS* sVl = lds + kOffVl;
+  char HK_LDS* sQh = lds + kOffQh;
+  char HK_LDS* sQl = lds + kOffQl;
+  char HK_LDS* sOh = lds + kOffOh;
+  char HK_LDS* sOl = lds + kOffOl;
+  char HK_LDS* sSh = lds + kOffSh;
+  char HK_LDS* sSl = lds + kOffSl;
+  float HK_LDS* sL = (float HK_LDS*)(lds + kOffL);
+  float HK_LDS* sD = (float HK_LDS*)(lds + kOffD);
 
   const int64_t T = p.T;
   // Linear order: all (batch, head)s of key tile 0 first, then key tile 1, ... Under causal
@@ -117,22 +207,22 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
 
   // K and V tiles (128 x 64) once
   {
-    float4 r[4];
-    load_rows<4>(Kb, p.k_strideM, k0, T, r);
-    store_rows<4>(sK, r);
-    load_rows<4>(Vb, p.v_strideM, k0, T, r);
-    store_rows<4>(sV, r);
+    Stager<kBKV> st;
+    st.load(Kb, p.k_strideM, k0, T);
+    st.store(sKh, sKl);
+    st.load(Vb, p.v_strideM, k0, T);
+    st.store(sVh, sVl);
   }
 
   // query tiles: causal starts at the tile holding the first key of this workgroup
   const int64_t q_first = p.is_causal ? (k0 / kBQ) * kBQ : 0;
   const int nq = static_cast<int>((T - q_first + kBQ - 1) / kBQ);
 
-  float4 rq[2], rdo[2];
+  Stager<kBQ> stq, sto;
   float rl = 0.f, rd = 0.f;
   auto fetch = [&](int64_t q0) {
-    load_rows<2>(Qb, p.q_strideM, q0, T, rq);
-    load_rows<2>(dOb, p.do_strideM, q0, T, rdo);
+    stq.load(Qb, p.q_strideM, q0, T);
+    sto.load(dOb, p.do_strideM, q0, T);
     if (threadIdx.x < kBQ) {
       const int64_t qq = q0 + threadIdx.x;
       rl = qq < T ? Lb[qq] * kLog2e : 0.f;
@@ -141,14 +231,23 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
   };
   if (nq > 0) fetch(q_first);
 
-  f32x16_t dv[2] = {f32x16_t{}, f32x16_t{}};  // dV: key 32 kg + 8(i/4) + 4hh + i%4, d 32db + c
+  // dV, dK: C layout of (A = P^T or dS^T: rows = keys, B = dO or Q: columns = d):
+  // key 32 kg + 8 (i/4) + 4 hh + i%4, d 32 db + c
+  f32x16_t dv[2] = {f32x16_t{}, f32x16_t{}};
   f32x16_t dk[2] = {f32x16_t{}, f32x16_t{}};
 
   for (int it = 0; it < nq; ++it) {
     const int64_t q0 = q_first + static_cast<int64_t>(it) * kBQ;
-    __syncthreads();  // previous tile's LDS reads are done
-    store_rows<2>(sQ, rq);
-    store_rows<2>(sdO, rdo);
+    // The LDS operand addresses below depend only on the lane; computed from this opaque copy
+    // they are formed inside the loop instead of being hoisted out of it, where ~100 of them
+    // would occupy registers for the whole kernel.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int c = ln & 31;
+    const int hh = ln >> 5;
+    __syncthreads();  // previous tile's LDS reads (and the dQ exchange) are done
+    stq.store(sQh, sQl);
+    sto.store(sOh, sOl);
     if (threadIdx.x < kBQ) {
       sL[threadIdx.x] = rl;
       sD[threadIdx.x] = rd;
@@ -156,55 +255,32 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
     __syncthreads();
     if (it + 1 < nq) fetch(q0 + kBQ);
 
-    // S = Q K^T and dP = dO V^T for this wave's 32 queries x 32 keys
+    // S = Q K^T and dP = dO V^T for this wave's 32 queries x 32 keys, contraction over d:
+    // lane (c, hh) holds key column 32 kg + c, queries 32 qh + 8 (i/4) + 4 hh + i%4.
     f32x16_t s = f32x16_t{}, dp = f32x16_t{};
-    {
-      const float* krow = sK + (32 * kg + c) * kPitch + 32 * hh;
-      const float* vrow = sV + (32 * kg + c) * kPitch + 32 * hh;
-      const float* qrow = sQ + (32 * qh + c) * kPitch + 32 * hh;
-      const float* orow = sdO + (32 * qh + c) * kPitch + 32 * hh;
-      // operands of step j + 1 are read while step j multiplies (two register stages)
-      float4 xa[2], xb[2];
-      xa[0] = *reinterpret_cast<const float4*>(qrow);
-      xb[0] = *reinterpret_cast<const float4*>(krow);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (j + 1 < 8) {
-          xa[(j + 1) & 1] = *reinterpret_cast<const float4*>(qrow + 4 * (j + 1));
-          xb[(j + 1) & 1] = *reinterpret_cast<const float4*>(krow + 4 * (j + 1));
-        } else {
-          xa[0] = *reinterpret_cast<const float4*>(orow);
-          xb[0] = *reinterpret_cast<const float4*>(vrow);
-        }
-        const float4 a = xa[j & 1], bb = xb[j & 1];
-        s = mfma(a.x, bb.x, s);
-        s = mfma(a.y, bb.y, s);
-        s = mfma(a.z, bb.z, s);
-        s = mfma(a.w, bb.w, s);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (j + 1 < 8) {
-          xa[(j + 1) & 1] = *reinterpret_cast<const float4*>(orow + 4 * (j + 1));
-          xb[(j + 1) & 1] = *reinterpret_cast<const float4*>(vrow + 4 * (j + 1));
-        }
-        const float4 a = xa[j & 1], bb = xb[j & 1];
-        dp = mfma(a.x, bb.x, dp);
-        dp = mfma(a.y, bb.y, dp);
-        dp = mfma(a.z, bb.z, dp);
-        dp = mfma(a.w, bb.w, dp);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    for (int ks = 0; ks < 4; ++ks) {
+      const int ch = 2 * ks + hh;
+      s = mfma3(rd_row(sQh, 32 * qh + c, ch), rd_row(sQl, 32 * qh + c, ch),
+                rd_row(sKh, 32 * kg + c, ch), rd_row(sKl, 32 * kg + c, ch), s);
+      __builtin_amdgcn_sched_barrier(0);  // keeps the operand reads of later steps from all
+                                          // being hoisted here (they would not fit registers)
     }
-    // P and dS in place: register i holds query q0 + 32 qh + 8 (i/4) + 4 hh + i%4.
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int ch = 2 * ks + hh;
+      dp = mfma3(rd_row(sOh, 32 * qh + c, ch), rd_row(sOl, 32 * qh + c, ch),
+                 rd_row(sVh, 32 * kg + c, ch), rd_row(sVl, 32 * kg + c, ch), dp);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // P and dS in place
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int qloc = 32 * qh + 8 * g + 4 * hh;
-      const float4 lv = *reinterpret_cast<const float4*>(sL + qloc);
-      const float4 dv4 = *reinterpret_cast<const float4*>(sD + qloc);
-      const float la[4] = {lv.x, lv.y, lv.z, lv.w};
-      const float da[4] = {dv4.x, dv4.y, dv4.z, dv4.w};
+      const f32x4_t lv = *reinterpret_cast<const f32x4_t HK_LDS*>(sL + qloc);
+      const f32x4_t dv4 = *reinterpret_cast<const f32x4_t HK_LDS*>(sD + qloc);
+      const float la[4] = {lv[0], lv[1], lv[2], lv[3]};
+      const float da[4] = {dv4[0], dv4[1], dv4[2], dv4[3]};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = 4 * g + e;
@@ -216,73 +292,72 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
         dp[i] = pv * (dp[i] - da[e]);
       }
     }
-    // dV += P^T dO, dK += dS^T Q (contraction over this wave's 32 queries). The dO / Q operands
-    // of query group g + 1 are read while group g multiplies; scheduling barriers keep the
-    // compiler from hoisting all 64 reads (which would spill).
+    // P^T / dS^T as A operands (rows = keys): k-step ks covers the lane's elements
+    // 8 ks .. 8 ks + 7, i.e. queries 32 qh + 16 ks + 4 hh + {0..3} and + 8 + {0..3}.
+    bf16x8_t ph[2], pl[2], sh[2], sl[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      float xs[8], xd[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xs[e] = s[8 * ks + e];
+        xd[e] = dp[8 * ks + e];
+      }
+      u32x4_t a, bq;
+      split8(xs, a, bq);
+      ph[ks] = as_bf16x8(a);
+      pl[ks] = as_bf16x8(bq);
+      split8(xd, a, bq);
+      sh[ks] = as_bf16x8(a);
+      sl[ks] = as_bf16x8(bq);
+    }
+    // dV += P^T dO, dK += dS^T Q: the dO / Q operand is read transposed (contraction over its
+    // rows = queries) in the same query order as the A operand.
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int r0 = 32 * qh + 16 * ks + 4 * hh, r1 = r0 + 8;
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        dv[db] = mfma3(ph[ks], pl[ks], rd_tr(sOh, 32 * db, r0, r1, ln),
+                       rd_tr(sOl, 32 * db, r0, r1, ln), dv[db]);
+        dk[db] = mfma3(sh[ks], sl[ks], rd_tr(sQh, 32 * db, r0, r1, ln),
+                       rd_tr(sQl, 32 * db, r0, r1, ln), dk[db]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // dS^T -> LDS [key][query]: the lane's 4 consecutive queries of group g are one 8-byte
+    // write per plane (already split: group g is half of A operand g / 2)
     {
-      float og[2][2][4], qg[2][2][4];
-      // per-lane bases; every read below is base + a compile-time offset (one LDS immediate)
-      const float* obase = sdO + (32 * qh + 4 * hh) * kPitch + c;
-      const float* qbase = sQ + (32 * qh + 4 * hh) * kPitch + c;
-      auto rd = [&](int g, int buf) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int db = 0; db < 2; ++db) {
-            og[buf][db][e] = obase[(8 * g + e) * kPitch + 32 * db];
-            qg[buf][db][e] = qbase[(8 * g + e) * kPitch + 32 * db];
-          }
-      };
-      rd(0, 0);
+      const int krow = 32 * kg + c;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        if (g + 1 < 4) rd(g + 1, (g + 1) & 1);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int db = 0; db < 2; ++db) {
-            dv[db] = mfma(s[4 * g + e], og[g & 1][db][e], dv[db]);
-            dk[db] = mfma(dp[4 * g + e], qg[g & 1][db][e], dk[db]);
-          }
-        __builtin_amdgcn_sched_barrier(0);
+        const int qc = 32 * qh + 8 * g + 4 * hh;  // first query of the group
+        const int off = off128(krow, qc >> 3) + (qc & 7) * 2;
+        const u32x4_t hv = __builtin_bit_cast(u32x4_t, sh[g >> 1]);
+        const u32x4_t lv = __builtin_bit_cast(u32x4_t, sl[g >> 1]);
+        const int half = g & 1;
+        *reinterpret_cast<u32x2_t HK_LDS*>(sSh + off) = u32x2_t{hv[2 * half], hv[2 * half + 1]};
+        *reinterpret_cast<u32x2_t HK_LDS*>(sSl + off) = u32x2_t{lv[2 * half], lv[2 * half + 1]};
       }
-    }
-    // dS -> LDS as [query][key]
-    {
-      float* sbase = sdS + (32 * qh + 4 * hh) * kSPitch + 32 * kg + c;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sbase[(8 * (i >> 2) + (i & 3)) * kSPitch] = dp[i];
     }
     __syncthreads();
-    // dQ block (queries 32 qb.., d 32 db..), key half kh of this wave = dS[q][keys] K[keys][d]
+    // dQ block (queries 32 qb.., d 32 db..), key half kh of this wave = dS[q][keys] K[keys][d]:
+    // both operands are read transposed (contraction over their rows = keys).
     const int qb = (wave >> 1) & 1, db = wave & 1, kh = wave >> 2;
     f32x16_t dq = f32x16_t{};
-    {
-      const float* srow = sdS + (32 * qb + c) * kSPitch + 64 * kh + 32 * hh;
-      const float* kcol = sK + (64 * kh + 32 * hh) * kPitch + 32 * db + c;
-      float4 sf[2];
-      float kk[2][4];
-      auto rd = [&](int j, int buf) {
-        sf[buf] = *reinterpret_cast<const float4*>(srow + 4 * j);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) kk[buf][e] = kcol[(4 * j + e) * kPitch];
-      };
-      rd(0, 0);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (j + 1 < 8) rd(j + 1, (j + 1) & 1);
-        const float4 a = sf[j & 1];
-        dq = mfma(a.x, kk[j & 1][0], dq);
-        dq = mfma(a.y, kk[j & 1][1], dq);
-        dq = mfma(a.z, kk[j & 1][2], dq);
-        dq = mfma(a.w, kk[j & 1][3], dq);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    for (int ks = 0; ks < 4; ++ks) {
+      const int r0 = 64 * kh + 16 * ks + 8 * hh, r1 = r0 + 4;
+      dq = mfma3(rd_tr(sSh, 32 * qb, r0, r1, ln), rd_tr(sSl, 32 * qb, r0, r1, ln),
+                 rd_tr(sKh, 32 * db, r0, r1, ln), rd_tr(sKl, 32 * db, r0, r1, ln), dq);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // key half 1 parks its partial in the Q tile's LDS (no longer read this tile); key half 0
-    // adds it and issues the atomics.
-    float* park = sQ + (wave & 3) * (32 * 33);
-    float* pbase = park + 4 * hh * 33 + c;
+    // dq layout: query 32 qb + 8 (i/4) + 4 hh + i%4, d 32 db + c. Key half 1 parks its
+    // partial in the Q / dO planes (not read again this tile); key half 0 adds it and issues
+    // the atomics.
+    float HK_LDS* park = (float HK_LDS*)(lds + kOffQh) + (wave & 3) * (32 * 33);
+    float HK_LDS* pbase = park + 4 * hh * 33 + c;
+    __syncthreads();  // every wave is done reading the Q / dO planes
     if (kh == 1) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) pbase[(8 * (i >> 2) + (i & 3)) * 33] = dq[i];
@@ -301,10 +376,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
     }
   }
 
-  // Sum the two query halves' dK / dV partials of each key group through LDS (the K/V tiles
-  // are no longer needed), then store dK (scaled) and dV rows of this wave's keys.
+  // Sum the two query halves' dK / dV partials of each key group through LDS (the tiles are no
+  // longer needed), then store dK (scaled) and dV rows of this wave's keys.
   __syncthreads();
-  float* pk = lds + kg * (2 * 32 * 65);  // [2 (dk, dv)][32 keys][65]
+  float HK_LDS* pk = (float HK_LDS*)lds + kg * (2 * 32 * 65);  // [2 (dk, dv)][32 keys][65]
   if (qh == 1) {
 #pragma unroll
     for (int d2 = 0; d2 < 2; ++d2)
