@@ -236,15 +236,51 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
   f32x16_t dv[2] = {f32x16_t{}, f32x16_t{}};
   f32x16_t dk[2] = {f32x16_t{}, f32x16_t{}};
 
+  // ---- per-lane LDS byte offsets, formed once; each read below adds compile-time or
+  // wave-uniform terms only -------------------------------------------------------------------
+  // Rows R + c (R a multiple of 32) share swz(c). 16-byte reads of chunk 2 ks + hh:
+  const int sw_c = swz(c);
+  int roff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) roff[ks] = c * kRowBytes + (((2 * ks + hh) ^ sw_c) << 4);
+  // Transposed reads: lane (group bit g1, index j) addresses row rb + j / 4 at column
+  // cb + 16 g1 + 4 (j % 4); x = chunk of that column within a 32-column block.
+  const int j15 = lane & 15, jj = j15 >> 2;
+  const int colin = 16 * ((lane >> 4) & 1) + 4 * (j15 & 3);
+  const int x = colin >> 3, colb = (colin & 7) * 2;
+  const int sbit = ((jj >> 1) & 1) << 2;
+  // dV / dK: rows 32 qh + 16 ks + 4 hh + {0..3} (elements 0-3) and + 8 (elements 4-7),
+  // columns 32 db + ...
+  int tva[2], tvb[2];
+#pragma unroll
+  for (int db = 0; db < 2; ++db) {
+    tva[db] = (4 * hh + jj) * kRowBytes + (((4 * db + x) ^ (sbit | hh)) << 4) + colb;
+    tvb[db] = (4 * hh + 8 + jj) * kRowBytes + (((4 * db + x) ^ (sbit | ((hh + 2) & 3))) << 4) + colb;
+  }
+  // dQ: rows 64 kh + 16 ks + 8 hh + {0..3} and + 4; dS^T columns 32 qb + ..., K columns 32 db + ...
+  const int qb = (wave >> 1) & 1, dbq = wave & 1, kh = wave >> 2;
+  const int tsa = (8 * hh + jj) * kRowBytes + (((4 * qb + x) ^ (sbit | (2 * hh))) << 4) + colb;
+  const int tsb = (8 * hh + 4 + jj) * kRowBytes + (((4 * qb + x) ^ (sbit | (2 * hh + 1))) << 4) + colb;
+  const int tka = (8 * hh + jj) * kRowBytes + (((4 * dbq + x) ^ (sbit | (2 * hh))) << 4) + colb;
+  const int tkb = (8 * hh + 4 + jj) * kRowBytes + (((4 * dbq + x) ^ (sbit | (2 * hh + 1))) << 4) + colb;
+  // dS^T writes: row 32 kg + c, queries 32 qh + 8 g + 4 hh .. + 3
+  int wsd[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) wsd[g] = c * kRowBytes + (((4 * qh + g) ^ sw_c) << 4) + 8 * hh;
+
+  const char HK_LDS* qrow = lds + kOffQh + 32 * qh * kRowBytes;  // + plane step for lo / dO
+  const char HK_LDS* krow = lds + kOffKh + 32 * kg * kRowBytes;
+  auto rd16 = [&](const char HK_LDS* base, int off) {
+    return *reinterpret_cast<const bf16x8_t HK_LDS*>(base + off);
+  };
+  auto rdtr = [&](const char HK_LDS* base, int offa, int offb) {
+    const bf16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bf16x4_t HK_LDS*)(base + offa));
+    const bf16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bf16x4_t HK_LDS*)(base + offb));
+    return bf16x8_t{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  };
+
   for (int it = 0; it < nq; ++it) {
     const int64_t q0 = q_first + static_cast<int64_t>(it) * kBQ;
-    // The LDS operand addresses below depend only on the lane; computed from this opaque copy
-    // they are formed inside the loop instead of being hoisted out of it, where ~100 of them
-    // would occupy registers for the whole kernel.
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
-    const int c = ln & 31;
-    const int hh = ln >> 5;
     __syncthreads();  // previous tile's LDS reads (and the dQ exchange) are done
     stq.store(sQh, sQl);
     sto.store(sOh, sOl);
@@ -255,104 +291,113 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
     __syncthreads();
     if (it + 1 < nq) fetch(q0 + kBQ);
 
-    // S = Q K^T and dP = dO V^T for this wave's 32 queries x 32 keys, contraction over d:
-    // lane (c, hh) holds key column 32 kg + c, queries 32 qh + 8 (i/4) + 4 hh + i%4.
-    f32x16_t s = f32x16_t{}, dp = f32x16_t{};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int ch = 2 * ks + hh;
-      s = mfma3(rd_row(sQh, 32 * qh + c, ch), rd_row(sQl, 32 * qh + c, ch),
-                rd_row(sKh, 32 * kg + c, ch), rd_row(sKl, 32 * kg + c, ch), s);
-      __builtin_amdgcn_sched_barrier(0);  // keeps the operand reads of later steps from all
-                                          // being hoisted here (they would not fit registers)
-    }
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int ch = 2 * ks + hh;
-      dp = mfma3(rd_row(sOh, 32 * qh + c, ch), rd_row(sOl, 32 * qh + c, ch),
-                 rd_row(sVh, 32 * kg + c, ch), rd_row(sVl, 32 * kg + c, ch), dp);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // P and dS in place
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int qloc = 32 * qh + 8 * g + 4 * hh;
-      const f32x4_t lv = *reinterpret_cast<const f32x4_t HK_LDS*>(sL + qloc);
-      const f32x4_t dv4 = *reinterpret_cast<const f32x4_t HK_LDS*>(sD + qloc);
-      const float la[4] = {lv[0], lv[1], lv[2], lv[3]};
-      const float da[4] = {dv4[0], dv4[1], dv4[2], dv4[3]};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 4 * g + e;
-        const int64_t qq = q0 + qloc + e;
-        const bool valid = qq < T && key < T && (!p.is_causal || key <= qq);
-        // exponent <= ~0 (scores minus the row's log-sum-exp); hardware exp2
-        const float pv = valid ? __builtin_amdgcn_exp2f(s[i] * sl2 - la[e]) : 0.f;
-        s[i] = pv;
-        dp[i] = pv * (dp[i] - da[e]);
-      }
-    }
-    // P^T / dS^T as A operands (rows = keys): k-step ks covers the lane's elements
-    // 8 ks .. 8 ks + 7, i.e. queries 32 qh + 16 ks + 4 hh + {0..3} and + 8 + {0..3}.
+    // This wave's block: keys k0 + 32 kg .. + 31, queries q0 + 32 qh .. + 31. Under causal
+    // masking a block whose keys all follow its queries is zero; one whose keys all precede
+    // them (and lies inside T) needs no mask.
+    const int64_t kw = k0 + 32 * kg, qw = q0 + 32 * qh;
+    const bool dead = p.is_causal && kw > qw + 31;
+    const bool clean = (!p.is_causal || kw + 31 <= qw) && kw + 32 <= T && qw + 32 <= T;
+
     bf16x8_t ph[2], pl[2], sh[2], sl[2];
+    if (!dead) {
+      // S = Q K^T and dP = dO V^T for this wave's 32 queries x 32 keys, contraction over d:
+      // lane (c, hh) holds key column 32 kg + c, queries 32 qh + 8 (i/4) + 4 hh + i%4.
+      f32x16_t s = f32x16_t{}, dp = f32x16_t{};
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      float xs[8], xd[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        xs[e] = s[8 * ks + e];
-        xd[e] = dp[8 * ks + e];
+      for (int ks = 0; ks < 4; ++ks) {
+        s = mfma3(rd16(qrow, roff[ks]), rd16(qrow + kQPlane, roff[ks]), rd16(krow, roff[ks]),
+                  rd16(krow + kKPlane, roff[ks]), s);
+        __builtin_amdgcn_sched_barrier(0);  // keeps the operand reads of later steps from all
+                                            // being hoisted here (they would not fit registers)
       }
-      u32x4_t a, bq;
-      split8(xs, a, bq);
-      ph[ks] = as_bf16x8(a);
-      pl[ks] = as_bf16x8(bq);
-      split8(xd, a, bq);
-      sh[ks] = as_bf16x8(a);
-      sl[ks] = as_bf16x8(bq);
-    }
-    // dV += P^T dO, dK += dS^T Q: the dO / Q operand is read transposed (contraction over its
-    // rows = queries) in the same query order as the A operand.
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int r0 = 32 * qh + 16 * ks + 4 * hh, r1 = r0 + 8;
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        dv[db] = mfma3(ph[ks], pl[ks], rd_tr(sOh, 32 * db, r0, r1, ln),
-                       rd_tr(sOl, 32 * db, r0, r1, ln), dv[db]);
-        dk[db] = mfma3(sh[ks], sl[ks], rd_tr(sQh, 32 * db, r0, r1, ln),
-                       rd_tr(sQl, 32 * db, r0, r1, ln), dk[db]);
+      for (int ks = 0; ks < 4; ++ks) {
+        dp = mfma3(rd16(qrow + 2 * kQPlane, roff[ks]), rd16(qrow + 3 * kQPlane, roff[ks]),
+                   rd16(krow + 2 * kKPlane, roff[ks]), rd16(krow + 3 * kKPlane, roff[ks]), dp);
         __builtin_amdgcn_sched_barrier(0);
       }
+      // P and dS in place
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int qloc = 32 * qh + 8 * g + 4 * hh;
+        const f32x4_t lv = *reinterpret_cast<const f32x4_t HK_LDS*>(sL + qloc);
+        const f32x4_t dv4 = *reinterpret_cast<const f32x4_t HK_LDS*>(sD + qloc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * g + e;
+          // exponent <= ~0 (scores minus the row's log-sum-exp); hardware exp2
+          float pv = __builtin_amdgcn_exp2f(s[i] * sl2 - lv[e]);
+          if (!clean) {
+            const int64_t qq = q0 + qloc + e;
+            const bool valid = qq < T && key < T && (!p.is_causal || key <= qq);
+            pv = valid ? pv : 0.f;
+          }
+          s[i] = pv;
+          dp[i] = pv * (dp[i] - dv4[e]);
+        }
+      }
+      // P^T / dS^T as A operands (rows = keys): k-step ks covers the lane's elements
+      // 8 ks .. 8 ks + 7, i.e. queries 32 qh + 16 ks + 4 hh + {0..3} and + 8 + {0..3}.
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        float xs[8], xd[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          xs[e] = s[8 * ks + e];
+          xd[e] = dp[8 * ks + e];
+        }
+        u32x4_t a, bq;
+        split8(xs, a, bq);
+        ph[ks] = as_bf16x8(a);
+        pl[ks] = as_bf16x8(bq);
+        split8(xd, a, bq);
+        sh[ks] = as_bf16x8(a);
+        sl[ks] = as_bf16x8(bq);
+      }
+      // dV += P^T dO, dK += dS^T Q: the dO / Q operand is read transposed (contraction over
+      // its rows = queries) in the same query order as the A operand.
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          const char HK_LDS* qb0 = qrow + ks * 16 * kRowBytes;
+          dv[db] = mfma3(ph[ks], pl[ks], rdtr(qb0 + 2 * kQPlane, tva[db], tvb[db]),
+                         rdtr(qb0 + 3 * kQPlane, tva[db], tvb[db]), dv[db]);
+          dk[db] = mfma3(sh[ks], sl[ks], rdtr(qb0, tva[db], tvb[db]),
+                         rdtr(qb0 + kQPlane, tva[db], tvb[db]), dk[db]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) ph[ks] = pl[ks] = sh[ks] = sl[ks] = bf16x8_t{};
     }
     // dS^T -> LDS [key][query]: the lane's 4 consecutive queries of group g are one 8-byte
     // write per plane (already split: group g is half of A operand g / 2)
     {
-      const int krow = 32 * kg + c;
+      char HK_LDS* wh = sSh + 32 * kg * kRowBytes;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int qc = 32 * qh + 8 * g + 4 * hh;  // first query of the group
-        const int off = off128(krow, qc >> 3) + (qc & 7) * 2;
         const u32x4_t hv = __builtin_bit_cast(u32x4_t, sh[g >> 1]);
         const u32x4_t lv = __builtin_bit_cast(u32x4_t, sl[g >> 1]);
         const int half = g & 1;
-        *reinterpret_cast<u32x2_t HK_LDS*>(sSh + off) = u32x2_t{hv[2 * half], hv[2 * half + 1]};
-        *reinterpret_cast<u32x2_t HK_LDS*>(sSl + off) = u32x2_t{lv[2 * half], lv[2 * half + 1]};
+        *reinterpret_cast<u32x2_t HK_LDS*>(wh + wsd[g]) = u32x2_t{hv[2 * half], hv[2 * half + 1]};
+        *reinterpret_cast<u32x2_t HK_LDS*>(wh + kKPlane + wsd[g]) =
+            u32x2_t{lv[2 * half], lv[2 * half + 1]};
       }
     }
     __syncthreads();
-    // dQ block (queries 32 qb.., d 32 db..), key half kh of this wave = dS[q][keys] K[keys][d]:
+    // dQ block (queries 32 qb.., d 32 dbq..), key half kh of this wave = dS[q][keys] K[keys][d]:
     // both operands are read transposed (contraction over their rows = keys).
-    const int qb = (wave >> 1) & 1, db = wave & 1, kh = wave >> 2;
     f32x16_t dq = f32x16_t{};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const int r0 = 64 * kh + 16 * ks + 8 * hh, r1 = r0 + 4;
-      dq = mfma3(rd_tr(sSh, 32 * qb, r0, r1, ln), rd_tr(sSl, 32 * qb, r0, r1, ln),
-                 rd_tr(sKh, 32 * db, r0, r1, ln), rd_tr(sKl, 32 * db, r0, r1, ln), dq);
+      const int rb = (64 * kh + 16 * ks) * kRowBytes;
+      dq = mfma3(rdtr(sSh + rb, tsa, tsb), rdtr(sSl + rb, tsa, tsb), rdtr(sKh + rb, tka, tkb),
+                 rdtr(sKl + rb, tka, tkb), dq);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // dq layout: query 32 qb + 8 (i/4) + 4 hh + i%4, d 32 db + c. Key half 1 parks its
+    // dq layout: query 32 qb + 8 (i/4) + 4 hh + i%4, d 32 dbq + c. Key half 1 parks its
     // partial in the Q / dO planes (not read again this tile); key half 0 adds it and issues
     // the atomics.
     float HK_LDS* park = (float HK_LDS*)(lds + kOffQh) + (wave & 3) * (32 * 33);
@@ -364,14 +409,17 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
     }
     __syncthreads();
     if (kh == 0) {
-      // per-lane row base; the per-register row steps (8 (i/4) + i%4) * stride are uniform
-      const int64_t qrow0 = q0 + 32 * qb + 4 * hh;
-      float* dqp = dQb + qrow0 * p.dq_strideM + 32 * db + c;
+      // wave-uniform row base plus a 32-bit per-lane offset (row 4 hh, column c); the
+      // per-register row steps (8 (i/4) + i%4) * stride are uniform too
+      const int64_t qblk = q0 + 32 * qb;
+      float* dqu = dQb + qblk * p.dq_strideM + 32 * dbq;
+      const int loff = static_cast<int>(4 * hh * p.dq_strideM) + c;
+      const bool rows_in = qblk + 32 <= T;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int rs = 8 * (i >> 2) + (i & 3);
-        if (qrow0 + rs < T)
-          unsafeAtomicAdd(dqp + rs * p.dq_strideM, (dq[i] + pbase[rs * 33]) * p.scale);
+        if (rows_in || qblk + 4 * hh + rs < T)
+          unsafeAtomicAdd(dqu + rs * p.dq_strideM + loff, (dq[i] + pbase[rs * 33]) * p.scale);
       }
     }
   }
@@ -431,6 +479,7 @@ extern "C" hipError_t hk_attn_backward(const hk_attn_bwd_params* params, int hea
                rows_aligned(p.dO, p.do_strideB, p.do_strideH, p.do_strideM));
   const int64_t bh = static_cast<int64_t>(p.B) * p.nh;
   HK_CHECK_ARG(bh <= 65535);
+  HK_CHECK_ARG(p.dq_strideM >= 0 && p.dq_strideM < (int64_t{1} << 28));  // 32-bit lane offsets
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
