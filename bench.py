@@ -379,7 +379,7 @@ def gemm_cases(g):
                             sb.data_ptr(), S["N"], 0, 0.0, sc.data_ptr(), S["N"], 0,
                             sbias.data_ptr(), S["N"], 1, S["split_k"], stream()) == 0
     cases.append(("sgemm_NN_4096^3_splitk4_bias", run_sgemm,
-                  W.gemm_flop(S["M"], S["N"], S["K"]), "fp32_matrix"))
+                  W.gemm_flop(S["M"], S["N"], S["K"]), "bf16x3"))
     return cases
 
 

@@ -613,6 +613,33 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
 
 }  // namespace
 
+namespace hk {
+
+void bgemm_split_plan(int M, int N, int K, int batch, int* used, int* kps) {
+  const int64_t tiles = static_cast<int64_t>((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  const int s = auto_split_k(tiles * batch, hk::ceil_div(K, BK), static_cast<int64_t>(M) * N * batch);
+  *kps = static_cast<int>(hk::ceil_div(hk::ceil_div(K, s), BK) * BK);
+  *used = static_cast<int>(hk::ceil_div(K, *kps));
+}
+
+hipError_t bgemm_partials(bool ta, bool tb, int M, int N, int K, const hk_bf16* A, int64_t lda,
+                          int64_t sA, const hk_bf16* B, int64_t ldb, int64_t sB, int batch,
+                          int used, int kps, float* part, hipStream_t stream) {
+  const int contig_a = ta ? M : K, contig_b = tb ? K : N;
+  HK_CHECK_ARG(M > 0 && N > 0 && K > 0 && batch > 0 && used >= 1 && kps % BK == 0);
+  HK_CHECK_ARG(contig_a % 8 == 0 && contig_b % 8 == 0 && N % 8 == 0 && lda % 8 == 0 &&
+               ldb % 8 == 0 && sA % 8 == 0 && sB % 8 == 0 && hk::aligned16(A) &&
+               hk::aligned16(B) && lda < (1 << 22) && ldb < (1 << 22));
+  const int64_t tiles = static_cast<int64_t>((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  HK_CHECK_ARG(tiles <= INT32_MAX && static_cast<int64_t>(batch) * used <= 65535);
+  const Epi ep{1.0f, 0.0f, nullptr, 0, 0};
+  dim3 grid(static_cast<unsigned>(tiles), 1, batch * used);
+  return dispatch_layout<true>(ta, tb, grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB, nullptr,
+                               0, 0, used, kps, part);
+}
+
+}  // namespace hk
+
 extern "C" hipError_t hk_bgemm(int transA, int transB, int M, int N, int K, hk_bf16 alpha,
                                const hk_bf16* A, int lda, long long strideA, const hk_bf16* B,
                                int ldb, long long strideB, hk_bf16 beta, hk_bf16* C, int ldc,

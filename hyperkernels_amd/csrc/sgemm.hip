@@ -10,12 +10,18 @@
 //       C = alpha * A B + beta * C + beta * bias, bias selected by bias_numel (1, N, M*N).
 //   tile-specialised kernels (sgemm_nn_256x128_..., sgemm_nt_..., sgemm_tn_...): the same
 //       product without bias for one layout each; splitK where the reference has it.
-// The reference multiplies with single-pass TF32 MMA; gfx950 has no TF32 matrix instruction, so
-// this file uses the full-precision fp32 MFMA (v_mfma_f32_32x32x2_f32): products are exact fp32
-// and only the summation order differs from a naive fp32 loop. The roofline for this path is
-// MI355X's fp32 matrix peak (157.3 TFLOP/s).
+// The reference multiplies with single-pass TF32 MMA; gfx950 has no TF32 matrix instruction.
+// Two paths:
+//   bf16x3 (shapes whose dimensions are multiples of 8, the common case): A and B are split into
+//     bf16 hi / lo operands over a tripled k axis (split3) so that one bf16 GEMM on the BF16 GEMM
+//     tiles of this library (bgemm.hip) sums ah bh + ah bl + al bh in fp32; the split-K
+//     finalize below applies alpha, beta and the bias. Relative error ~1e-5 (max-rel 3e-6 at
+//     4096^3 against a float64 product) at bf16 MFMA rate: 4096^3 + bias in ~0.57 ms against
+//     ~1.17 ms on the fp32 MFMA. Roofline: the bf16 peak / 3 (three products per fp32 product).
+//   fp32 MFMA tiles (other 4-element-aligned shapes): v_mfma_f32_32x32x2_f32, exact fp32
+//     products; roofline the fp32 matrix peak (157.3 TFLOP/s).
 //
-// Design (gfx950): the same tiling as the BF16 GEMM of this library - 256 x 256 workgroup
+// Design of the fp32 tiles (gfx950): the same tiling as the BF16 GEMM of this library - 256 x 256 workgroup
 // tile, 4 waves of 128 x 128 (4 x 4 MFMA tiles, 256 fp32 accumulators per lane), k-tiles of
 // 32 fp32 copied HBM/L2 -> LDS without passing through registers (global_load_lds_dwordx4)
 // into a 2-stage LDS ring, one barrier per k-tile. K-major operands sit in LDS as [row][k]
@@ -384,6 +390,45 @@ __global__ __launch_bounds__(256) void sgemm_simple(int ta, int tb, int M, int N
   *dst = f;
 }
 
+// bf16x3 operand of an fp32 matrix X (rows x cols, leading dimension ldx, batch stride sx):
+// each x = hi + lo (bf16, round to nearest even, |x - hi - lo| <= 2^-18 |x|) and the k axis is
+// tripled into three segments, (hi, hi, lo) for the left operand and (hi, lo, hi) for the right,
+// so that a bf16 GEMM over 3K sums ah bh + ah bl + al bh. KCOLS: k runs along the columns
+// (Y[r][s cols + c]); otherwise along the rows (Y[s rows + r][c]). Four columns per thread
+// (cols % 4 == 0, 16-byte aligned rows).
+template <bool KCOLS>
+__global__ __launch_bounds__(256) void split3(const float* __restrict__ X, int64_t ldx, int64_t sx,
+                                              int rows, int cols, uint16_t* __restrict__ Y,
+                                              int64_t ldy, int64_t sy, int left, int batch) {
+  const int c4 = cols >> 2;
+  const int64_t per = static_cast<int64_t>(rows) * c4;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= per * batch) return;
+  const int b = static_cast<int>(i / per);
+  const int64_t e = i - b * per;
+  const int r = static_cast<int>(e / c4), c = static_cast<int>(e - static_cast<int64_t>(r) * c4) * 4;
+  const f32x4_t v = *reinterpret_cast<const f32x4_t*>(X + b * sx + static_cast<int64_t>(r) * ldx + c);
+  uint32_t hv[2], lv[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const float x0 = v[2 * k], x1 = v[2 * k + 1];
+    const uint16_t h0 = hk::f32_to_bf16(x0), h1 = hk::f32_to_bf16(x1);
+    const uint16_t l0 = hk::f32_to_bf16(x0 - hk::bf16_to_f32(h0));
+    const uint16_t l1 = hk::f32_to_bf16(x1 - hk::bf16_to_f32(h1));
+    hv[k] = h0 | (static_cast<uint32_t>(h1) << 16);
+    lv[k] = l0 | (static_cast<uint32_t>(l1) << 16);
+  }
+  const uint2 H = make_uint2(hv[0], hv[1]), L = make_uint2(lv[0], lv[1]);
+  uint16_t* Yb = Y + b * sy;
+  const uint2 seg[3] = {H, left ? H : L, left ? L : H};
+#pragma unroll
+  for (int sg = 0; sg < 3; ++sg) {
+    uint16_t* dst = KCOLS ? Yb + static_cast<int64_t>(r) * ldy + sg * cols + c
+                          : Yb + (static_cast<int64_t>(sg) * rows + r) * ldy + c;
+    *reinterpret_cast<uint2*>(dst) = seg[sg];
+  }
+}
+
 template <bool AK, bool BKM, bool P>
 hipError_t launch_tiled(dim3 grid, hipStream_t stream, int M, int N, int K, const float* A,
                         int64_t lda, int64_t sA, const float* B, int64_t ldb, int64_t sB,
@@ -447,6 +492,56 @@ hipError_t sgemm_run(bool ta, bool tb, int M, int N, int K, float alpha, const f
     hipLaunchKernelGGL(sgemm_simple, grid, dim3(256), 0, stream, ta ? 1 : 0, tb ? 1 : 0, M, N, K,
                        A, static_cast<int64_t>(lda), static_cast<int64_t>(strideA), B,
                        static_cast<int64_t>(ldb), static_cast<int64_t>(strideB), C,
+                       static_cast<int64_t>(ldc), static_cast<int64_t>(strideC), ep);
+    return hk::launch_status();
+  }
+  // bf16x3 on the BF16 GEMM tiles when every dimension the split copies touch is a multiple
+  // of 8: A and B are split into bf16 hi / lo operands over a tripled k axis, multiplied into
+  // fp32 partials and finished (alpha, beta, bias once) by the split-K finalize. The split-K
+  // of the call is a work-partition hint; this path picks its own.
+  const bool x3_ok = K % 8 == 0 && N % 8 == 0 && (!ta || M % 8 == 0) &&
+                     3LL * K < (1 << 22) && (ta ? M : 3LL * K) < (1 << 22) &&
+                     (tb ? 3LL * K : N) < (1 << 22);
+  if (x3_ok) {
+    const int K3 = 3 * K;
+    // A' is [M][3K] (k-major) or [3K][M]; B' is [3K][N] or [N][3K]
+    const int64_t la = ta ? M : K3, lb = tb ? K3 : N;
+    const int64_t na = static_cast<int64_t>(M) * K3, nb = static_cast<int64_t>(K3) * N;
+    int used = 1, kps = 0;
+    hk::bgemm_split_plan(M, N, K3, batchCount, &used, &kps);
+    auto up = [](int64_t bytes) { return (bytes + 255) & ~int64_t{255}; };
+    const int64_t a_bytes = up(na * batchCount * 2), b_bytes = up(nb * batchCount * 2);
+    const int64_t p_bytes = static_cast<int64_t>(used) * batchCount * M * N * 4;
+    void* ws = nullptr;
+    HK_RETURN_IF_ERROR(hk::device_workspace(static_cast<size_t>(a_bytes + b_bytes + p_bytes),
+                                            stream, &ws));
+    uint16_t* A3 = static_cast<uint16_t*>(ws);
+    uint16_t* B3 = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + a_bytes);
+    float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + a_bytes + b_bytes);
+    // A: rows x cols as stored; k along columns when not transposed
+    {
+      const int rows = ta ? K : M, cols = ta ? M : K;
+      const int64_t n4 = static_cast<int64_t>(rows) * (cols / 4) * batchCount;
+      auto* k = ta ? split3<false> : split3<true>;
+      hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(hk::ceil_div(n4, 256))), dim3(256), 0,
+                         stream, A, static_cast<int64_t>(lda), static_cast<int64_t>(strideA), rows,
+                         cols, A3, la, na, 1, batchCount);
+      HK_RETURN_IF_ERROR(hk::launch_status());
+    }
+    {
+      const int rows = tb ? N : K, cols = tb ? K : N;
+      const int64_t n4 = static_cast<int64_t>(rows) * (cols / 4) * batchCount;
+      auto* k = tb ? split3<true> : split3<false>;
+      hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(hk::ceil_div(n4, 256))), dim3(256), 0,
+                         stream, B, static_cast<int64_t>(ldb), static_cast<int64_t>(strideB), rows,
+                         cols, B3, lb, nb, 0, batchCount);
+      HK_RETURN_IF_ERROR(hk::launch_status());
+    }
+    HK_RETURN_IF_ERROR(hk::bgemm_partials(ta, tb, M, N, K3, A3, la, na, B3, lb, nb, batchCount,
+                                          used, kps, part, stream));
+    const int64_t total = static_cast<int64_t>(M) * N * batchCount;
+    hipLaunchKernelGGL(sgemm_splitk_finalize, dim3(static_cast<unsigned>(hk::ceil_div(total, 256))),
+                       dim3(256), 0, stream, part, used, batchCount, M, N, C,
                        static_cast<int64_t>(ldc), static_cast<int64_t>(strideC), ep);
     return hk::launch_status();
   }

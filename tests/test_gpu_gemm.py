@@ -262,6 +262,21 @@ def test_sgemm_tile_kernel_entry_point(hk, orc, lay):
     assert max_rel(out, orc.sgemm(ta, tb, A, B, alpha=1.0, beta=0.5, C0=C0)) <= 2e-3
 
 
+@pytest.mark.parametrize("M,N,K,lay", [(260, 264, 100, "NN"), (260, 264, 100, "NT"),
+                                       (260, 264, 100, "TN"), (300, 256, 64, "TN")])
+@pytest.mark.parametrize("split_k", [1, 2])
+def test_sgemm_fp32_tile_path(hk, orc, M, N, K, lay, split_k):
+    # K (or M for TN) a multiple of 4 but not of 8: the fp32 MFMA tiles, not the bf16x3 path
+    enum, ta, tb = SG_LAYOUT[lay]
+    say("sgemm fp32 tiles", M, N, K, lay, split_k)
+    A, B, C0, bias = _sg_operands(orc, M, N, K, ta, tb, 900 + K)
+    out = _sg_call(hk, "hk_sgemm", enum, torch.from_numpy(A).to(DEV), torch.from_numpy(B).to(DEV),
+                   torch.from_numpy(C0).to(DEV), M, N, K, 1.5, 0.5,
+                   bias=torch.from_numpy(bias).to(DEV), bias_stride=N, split_k=split_k)
+    ref = orc.sgemm(ta, tb, A, B, alpha=1.5, beta=0.5, C0=C0, bias=bias)
+    assert max_rel(out, ref) <= 2e-3
+
+
 @pytest.mark.parametrize("M,N,K,lay", [(17, 9, 33, "NN"), (33, 65, 7, "TN"), (5, 300, 41, "NT")])
 def test_sgemm_ragged(hk, orc, M, N, K, lay):
     enum, ta, tb = SG_LAYOUT[lay]
