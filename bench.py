@@ -11,8 +11,10 @@ time (GB/s, the reference's byte conventions, README.md:186-199).
 `roofline` is for the step's dominant kernel (longest average duration), timed live with HIP
 events on the launch stream. `cpu_baseline` is the repository's CPU oracle (a restatement of
 the reference harnesses' CPU references) timed on this host on a bounded sample of the same
-step. `per_kernel` lists each kernel of the surface at its BASELINE config, timed alone
-(cache flushed between repetitions).
+step. `per_kernel` lists each kernel of the surface at its BASELINE config, timed alone: each
+repetition flushes the caches and times one burst of launches between one pair of events
+(memory-bound kernels: one launch per distinct buffer set, ~1 GiB touched in all, so every
+launch reads HBM; compute-bound kernels: 5 launches of the same operands).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--suite headline|all]
 """
@@ -86,6 +88,37 @@ def time_kernel(fn, reps, flush=None):
     torch.cuda.synchronize()
     ts = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
     return {"avg_ms": sum(ts) / len(ts), "median_ms": ts[len(ts) // 2], "min_ms": ts[0]}
+
+
+def time_burst(fns, reps, flush):
+    """Average duration (ms) of one launch in a burst: each repetition flushes the caches, then
+    launches every fn of `fns` back to back between one pair of events on the current stream
+    and divides by len(fns). For memory-bound kernels `fns` run on distinct buffer sets (each
+    set is read from HBM once per burst), for compute-bound ones they repeat one launch.
+    One event pair per burst keeps the ~5 us event overhead out of short kernels."""
+    for f in fns:
+        f()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    for i in range(reps):
+        flush()
+        starts[i].record()
+        for f in fns:
+            f()
+        ends[i].record()
+    torch.cuda.synchronize()
+    ts = sorted(s.elapsed_time(e) / len(fns) for s, e in zip(starts, ends))
+    return {"avg_ms": sum(ts) / len(ts), "median_ms": ts[len(ts) // 2], "min_ms": ts[0]}
+
+
+BURST_BYTES = 1 << 30  # a burst of memory-bound launches touches about this many distinct bytes
+COMPUTE_BURST = 5      # launches per burst of a compute-bound kernel
+
+
+def n_sets(footprint: int) -> int:
+    """Buffer sets for a memory-bound burst: enough that a burst touches ~1 GiB, at most 32."""
+    return max(1, min(32, -(-BURST_BYTES // max(footprint, 1))))
 
 
 # ------------------------------------------------------------------------------------------------
@@ -209,41 +242,42 @@ def per_kernel_suite(flush):
     out = {}
     g = torch.Generator(device=DEV)
     g.manual_seed(99)
-    # LayerNorm configs[0]
+    # LayerNorm configs[0], in fp32 and in bf16 / fp16 storage (fp32 statistics); gamma and
+    # beta are shared by the buffer sets
     R, C = W.LN["rows"], W.LN["cols"]
-    x = torch.randn(R, C, generator=g, device=DEV)
     gamma = torch.rand(C, generator=g, device=DEV) + 0.5
     beta = torch.randn(C, generator=g, device=DEV) * 0.1
-    dy = torch.randn(R, C, generator=g, device=DEV)
-    y, mean, rstd = hk.layer_norm_forward(x, gamma, beta, W.LN["eps"])
-    dx = torch.empty_like(x)
-    dgam = torch.zeros(C, device=DEV)
-    dbet = torch.zeros(C, device=DEV)
-    cases = [
-        ("ln_fwd", lambda: hk.layer_norm_forward(x, gamma, beta, W.LN["eps"], y, mean, rstd),
-         W.ln_fwd_bytes(R, C), "hbm"),
-        ("ln_bwd_fused", lambda: hk.layer_norm_backward(dy, x, mean, rstd, gamma, dgam, dbet, dx),
-         W.ln_bwd_bytes(R, C), "hbm"),
-    ]
-    # the same LayerNorm in bf16 and fp16 storage (fp32 statistics)
-    for dt, tag in ((torch.bfloat16, "bf16"), (torch.float16, "f16")):
-        x16, g16, b16, dy16 = x.to(dt), gamma.to(dt), beta.to(dt), dy.to(dt)
-        y16, dx16 = torch.empty_like(x16), torch.empty_like(x16)
-        cases += [
-            (f"ln_fwd_{tag}", lambda x16=x16, g16=g16, b16=b16, y16=y16: hk.layer_norm_forward(
-                x16, g16, b16, W.LN["eps"], y16, mean, rstd), W.ln_fwd_bytes(R, C, 2), "hbm"),
-            (f"ln_bwd_fused_{tag}", lambda dy16=dy16, x16=x16, g16=g16, dx16=dx16:
-                hk.layer_norm_backward(dy16, x16, mean, rstd, g16, dgam, dbet, dx16),
-             W.ln_bwd_bytes(R, C, 2), "hbm"),
-        ]
+    cases = []
+    for dt, tag, es in ((torch.float32, "", 4), (torch.bfloat16, "_bf16", 2),
+                        (torch.float16, "_f16", 2)):
+        g16, b16 = gamma.to(dt), beta.to(dt)
+        dgam = torch.zeros(C, device=DEV)
+        dbet = torch.zeros(C, device=DEV)
+        fwd, bwd = [], []
+        for _ in range(n_sets(W.ln_bwd_bytes(R, C, es))):
+            x = torch.randn(R, C, generator=g, device=DEV).to(dt)
+            dy = torch.randn(R, C, generator=g, device=DEV).to(dt)
+            y, dx = torch.empty_like(x), torch.empty_like(x)
+            mean = torch.empty(R, device=DEV)
+            rstd = torch.empty(R, device=DEV)
+            hk.layer_norm_forward(x, g16, b16, W.LN["eps"], y, mean, rstd)
+            fwd.append(lambda x=x, y=y, mean=mean, rstd=rstd, g16=g16, b16=b16:
+                       hk.layer_norm_forward(x, g16, b16, W.LN["eps"], y, mean, rstd))
+            bwd.append(lambda dy=dy, x=x, mean=mean, rstd=rstd, dx=dx, g16=g16, dgam=dgam,
+                       dbet=dbet: hk.layer_norm_backward(dy, x, mean, rstd, g16, dgam, dbet, dx))
+        cases += [(f"ln_fwd{tag}", fwd, W.ln_fwd_bytes(R, C, es), "hbm"),
+                  (f"ln_bwd_fused{tag}", bwd, W.ln_bwd_bytes(R, C, es), "hbm")]
     # GELU in fp16 at the configs[1] shape (the headline step runs the bf16 form)
     n = W.numel(W.GELU["shape"])
-    gx = torch.randn(n, generator=g, device=DEV).half()
-    gg = torch.randn(n, generator=g, device=DEV).half()
-    gy, gi = torch.empty_like(gx), torch.empty_like(gx)
-    cases += [("gelu_fwd_f16", lambda: hk.gelu_forward(gx, gy), W.gelu_fwd_bytes(n, 2), "hbm"),
-              ("gelu_bwd_f16", lambda: hk.gelu_backward(gg, gx, gi), W.gelu_bwd_bytes(n, 2),
-               "hbm")]
+    gf, gb = [], []
+    for _ in range(n_sets(W.gelu_bwd_bytes(n, 2))):
+        gx = torch.randn(n, generator=g, device=DEV).half()
+        gg = torch.randn(n, generator=g, device=DEV).half()
+        gy, gi = torch.empty_like(gx), torch.empty_like(gx)
+        gf.append(lambda gx=gx, gy=gy: hk.gelu_forward(gx, gy))
+        gb.append(lambda gg=gg, gx=gx, gi=gi: hk.gelu_backward(gg, gx, gi))
+    cases += [("gelu_fwd_f16", gf, W.gelu_fwd_bytes(n, 2), "hbm"),
+              ("gelu_bwd_f16", gb, W.gelu_bwd_bytes(n, 2), "hbm")]
     # unified reduce at the README shape
     rs = torch.randn(16384, 50304, generator=g, device=DEV)
     lay = hk.ReductionLayout()
@@ -256,7 +290,8 @@ def per_kernel_suite(flush):
     cases += gemv_cases(g)
     cases += attention_cases(g)
     for name, fn, work, bound in cases:
-        t = time_kernel(fn, ARGS.reps, flush)
+        fns = fn if isinstance(fn, list) else [fn] * (1 if bound == "hbm" else COMPUTE_BURST)
+        t = time_burst(fns, ARGS.reps, flush)
         if bound == "hbm":
             ach = work / (t["avg_ms"] * 1e-3) / 1e9
             out[name] = {"avg_ms": round(t["avg_ms"], 5), "achieved": round(ach, 1), "unit": "GB/s",
@@ -307,23 +342,29 @@ def gemv_cases(g):
     one, zero = 0x3F80, 0
     cases = []
     V, C = 50257, 768
-    x = torch.randn(C, generator=g, device=DEV).to(torch.bfloat16)
-    wte = (torch.randn(V, C, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
-    logits = torch.empty(V, device=DEV, dtype=torch.bfloat16)
+    nt = []
+    for _ in range(n_sets(2 * V * C)):
+        x = torch.randn(C, generator=g, device=DEV).to(torch.bfloat16)
+        wte = (torch.randn(V, C, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+        logits = torch.empty(V, device=DEV, dtype=torch.bfloat16)
 
-    def run_nt():
-        assert lib.hk_bgemv_nt_row(V, C, one, x.data_ptr(), wte.data_ptr(), C, zero,
-                                   logits.data_ptr(), 1, 0, 0, 0, stream()) == 0
-    cases.append(("bgemv_nt_row_50257x768", run_nt, 2 * V * C + 2 * (V + C), "hbm"))
+        def run_nt(x=x, wte=wte, logits=logits):
+            assert lib.hk_bgemv_nt_row(V, C, one, x.data_ptr(), wte.data_ptr(), C, zero,
+                                       logits.data_ptr(), 1, 0, 0, 0, stream()) == 0
+        nt.append(run_nt)
+    cases.append(("bgemv_nt_row_50257x768", nt, 2 * V * C + 2 * (V + C), "hbm"))
     K, N = 4096, 16384
-    xk = torch.randn(K, generator=g, device=DEV).to(torch.bfloat16)
-    w = (torch.randn(K, N, generator=g, device=DEV) * K ** -0.5).to(torch.bfloat16)
-    y = torch.empty(N, device=DEV, dtype=torch.bfloat16)
+    nn = []
+    for _ in range(n_sets(2 * K * N)):
+        xk = torch.randn(K, generator=g, device=DEV).to(torch.bfloat16)
+        w = (torch.randn(K, N, generator=g, device=DEV) * K ** -0.5).to(torch.bfloat16)
+        y = torch.empty(N, device=DEV, dtype=torch.bfloat16)
 
-    def run_nn():
-        assert lib.hk_bgemv_nn_row(N, K, one, xk.data_ptr(), w.data_ptr(), N, zero, y.data_ptr(),
-                                   1, 0, 0, 0, stream()) == 0
-    cases.append(("bgemv_nn_row_4096x16384", run_nn, 2 * K * N + 2 * (K + N), "hbm"))
+        def run_nn(xk=xk, w=w, y=y):
+            assert lib.hk_bgemv_nn_row(N, K, one, xk.data_ptr(), w.data_ptr(), N, zero,
+                                       y.data_ptr(), 1, 0, 0, 0, stream()) == 0
+        nn.append(run_nn)
+    cases.append(("bgemv_nn_row_4096x16384", nn, 2 * K * N + 2 * (K + N), "hbm"))
     return cases
 
 
