@@ -72,32 +72,45 @@ __device__ __forceinline__ void copy16_to_lds(const void* sbase, int voff, unsig
 
 // One operand of a k-tile in LDS: 256 rows of M (or N) by BK = 64 k, bf16, 32 KiB.
 //
+// gfx950's LDS has 64 banks of 4 bytes: a ds_read_b128 is served 16 lanes (256 bytes) per
+// cycle and a ds_read_b64(_tr) 32 lanes per cycle, so each such lane group must cover all 64
+// banks once (a 2-way conflict halves the read rate; measured 134 against 222 B/clk/CU).
+//
 // K-major operands (element (row, k) at base[row * ld + k]) are stored [row][64 k]: 128-byte
-// rows whose eight 16-byte chunks sit at chunk ^ (row & 7). A wave's copy instruction moves
-// 8 rows (lane l: row l / 8, stored chunk l % 8, which is global chunk (l % 8) ^ (row & 7), so
-// each row's 128 contiguous bytes are read by 8 lanes). The MFMA operand of a lane is 8
-// consecutive k of one row, one ds_read_b128; 8 consecutive lanes read 8 consecutive rows at
-// 8 distinct chunk positions, i.e. all 32 banks once.
+// rows whose eight 16-byte chunks sit at chunk ^ ((row >> 1) & 7). A wave's copy instruction
+// moves 8 rows (lane l: row l / 8, stored chunk l % 8, which is global chunk
+// (l % 8) ^ ((row >> 1) & 7), so each row's 128 contiguous bytes are read by 8 lanes). The
+// MFMA operand of a lane is 8 consecutive k of one row, one ds_read_b128; the 16 lanes of one
+// read cycle take 16 consecutive rows at one logical chunk: the even rows fill one 128-byte
+// bank half at 8 distinct chunk positions and the odd rows the other.
 //
 // M/N-major operands (element at base[k * ld + row]) are stored as in HBM, [64 k][256 rows]:
-// 512-byte k-rows whose 16-byte chunks sit at chunk ^ (2 * (krow & 3)). A copy instruction
-// moves 2 k-rows (32 lanes read one contiguous 512-byte row segment). The MFMA operand (8
-// consecutive k of one row/column) is gathered with two ds_read_b64_tr_b16: within each
-// 16-lane group, lane j reads 4 bf16 of k-row kb + j / 4 at columns c0 + 4 (j % 4) and the
-// hardware transposes the 16 x 4 block so lane i receives column c0 + i, k = kb .. kb + 3. The
-// 16 lanes of one read touch 4 k-rows x 32 bytes; the chunk permutation spreads them over all
-// 32 banks.
+// 512-byte k-rows whose 16-byte chunk c sits at c ^ (2 * (krow & 3)) ^ (8 * ((c >> 1) & 1)).
+// A copy instruction moves 2 k-rows (32 lanes read one contiguous 512-byte row segment). The
+// MFMA operand (8 consecutive k of one row/column) is gathered with two ds_read_b64_tr_b16:
+// within each 16-lane group, lane j reads 4 bf16 of k-row kb + j / 4 at columns
+// c0 + 4 (j % 4) and the hardware transposes the 16 x 4 block so lane i receives column
+// c0 + i, k = kb .. kb + 3. One group covers 4 k-rows x 32 bytes, which the (krow & 3) term
+// spreads over 32 banks; the two groups of a read cycle sit 16 columns (2 chunks) apart and
+// the (c >> 1) term places them in opposite bank halves.
 template <bool KMAJOR>
 struct TileOperand {
+  // M/N-major: stored position of logical 16-byte chunk c of k-row krow, and its inverse.
+  __device__ static int stored_chunk(int c, int krow) {
+    return c ^ (2 * (krow & 3)) ^ (8 * ((c >> 1) & 1));
+  }
+  __device__ static int logical_chunk(int p, int krow) {
+    return p ^ (8 * (((p >> 1) ^ krow) & 1)) ^ (2 * (krow & 3));
+  }
   // Byte offset of lane `lane`'s 16 bytes of copy instruction ii (0 .. 31) from the tile's
   // global base at k = 0, and the (row, k) of its first element.
   __device__ static void source(int ii, int lane, int64_t ld, int& row, int& k) {
     if (KMAJOR) {
       row = ii * 8 + (lane >> 3);
-      k = ((lane & 7) ^ (row & 7)) * 8;
+      k = ((lane & 7) ^ ((row >> 1) & 7)) * 8;
     } else {
       k = ii * 2 + (lane >> 5);
-      row = ((lane & 31) ^ (2 * (k & 3))) * 8;
+      row = logical_chunk(lane & 31, k) * 8;
     }
   }
   __device__ static int64_t byte_offset(int row, int k, int64_t ld) {
@@ -112,12 +125,12 @@ struct TileOperand {
     if (KMAJOR) {
       const int row = wo + b * 32 + (lane & 31);
       const int c = 2 * s + (lane >> 5);
-      return row * 128 + ((c ^ (row & 7)) * 16);
+      return row * 128 + ((c ^ ((row >> 1) & 7)) * 16);
     } else {
       const int g = lane >> 4, j = lane & 15;
       const int col = wo + b * 32 + 16 * (g & 1) + 4 * (j & 3);
       const int krow = 16 * s + 8 * (g >> 1) + (j >> 2) + 4 * half;
-      return krow * 512 + (((col >> 3) ^ (2 * (krow & 3))) * 16) + (col & 7) * 2;
+      return krow * 512 + stored_chunk(col >> 3, krow) * 16 + (col & 7) * 2;
     }
   }
   __device__ static bf16x8_t read(const unsigned char HK_LDS* st, int wo, int b, int s,
