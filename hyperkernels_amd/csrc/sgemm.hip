@@ -62,25 +62,29 @@ __device__ __forceinline__ void copy16_to_lds(const void* sbase, int voff, unsig
 }
 
 // One operand of a k-tile in LDS: 256 rows of M (or N) by BK = 32 k, fp32, 32 KiB.
+// gfx950's LDS has 64 banks of 4 bytes and serves 256 bytes per cycle: 16 lanes of a 16-byte
+// read, 64 lanes of a 4-byte read. Each such lane group must cover the 64 banks once.
 //
 // K-major operands (element (row, k) at base[row * ld + k]) are stored [row][32 k]: 128-byte
-// rows whose 16-byte chunks (4 k each) sit at chunk ^ (row & 7); a copy instruction moves 8
-// rows (lane l: row l / 8, stored chunk l % 8), 8 lanes per 128-byte HBM row segment. Lane
-// (r, h) of a wave feeds k = 16 h + s of the tile at MFMA step s, so it reads 16 consecutive k
-// of its row as four 16-byte LDS reads (chunks 4 h .. 4 h + 3); 8 consecutive rows at one chunk
-// position cover all 32 banks once.
+// rows whose 16-byte chunks (4 k each) sit at chunk ^ ((row >> 1) & 7); a copy instruction
+// moves 8 rows (lane l: row l / 8, stored chunk l % 8), 8 lanes per 128-byte HBM row segment.
+// Lane (r, h) of a wave feeds k = 16 h + s of the tile at MFMA step s, so it reads 16
+// consecutive k of its row as four 16-byte LDS reads (chunks 4 h .. 4 h + 3); 16 consecutive
+// rows at one chunk: the even rows fill one bank half at 8 distinct positions, the odd rows
+// the other.
 // M/N-major operands (element at base[k * ld + row]) are stored as in HBM, [32 k][256 rows]
-// (1 KiB per k-row, one copy instruction); the operand of MFMA step s is one float per lane,
-// row k = 16 h + s, 32 consecutive rows per half-wave (all 32 banks).
+// (1 KiB per k-row, one copy instruction), with the 16-byte chunks of k-rows 16 .. 31 at
+// chunk ^ 8; the operand of MFMA step s is one float per lane, row k = 16 h + s, 32
+// consecutive rows per half-wave, the two half-waves in opposite bank halves.
 template <bool KMAJOR>
 struct TileOperand {
   __device__ static void source(int ii, int lane, int& row, int& k) {
     if (KMAJOR) {
       row = ii * 8 + (lane >> 3);
-      k = ((lane & 7) ^ (row & 7)) * 4;
+      k = ((lane & 7) ^ ((row >> 1) & 7)) * 4;
     } else {
       k = ii;
-      row = lane * 4;
+      row = (lane ^ (8 * ((k >> 4) & 1))) * 4;
     }
   }
   __device__ static int64_t byte_offset(int row, int k, int64_t ld) {
@@ -94,10 +98,13 @@ struct TileOperand {
     const int r = wo + b * 32 + (lane & 31), h = lane >> 5;
     if (KMAJOR) {
       const int c = 4 * h + qd;
-      return *reinterpret_cast<const f32x4_t HK_LDS*>(st + r * 128 + ((c ^ (r & 7)) * 16));
+      return *reinterpret_cast<const f32x4_t HK_LDS*>(st + r * 128 +
+                                                      ((c ^ ((r >> 1) & 7)) * 16));
     } else {
+      // k-rows 16 h + 4 qd .. +3 all lie in one half (h), so one chunk flip serves the four
+      const int rs = r ^ (32 * h);
       const float HK_LDS* col =
-          reinterpret_cast<const float HK_LDS*>(st) + (16 * h + 4 * qd) * 256 + r;
+          reinterpret_cast<const float HK_LDS*>(st) + (16 * h + 4 * qd) * 256 + rs;
       return f32x4_t{col[0], col[256], col[512], col[768]};
     }
   }
