@@ -421,6 +421,18 @@ def gemm_cases(g):
                             sbias.data_ptr(), S["N"], 1, S["split_k"], stream()) == 0
     cases.append(("sgemm_NN_4096^3_splitk4_bias", run_sgemm,
                   W.gemm_flop(S["M"], S["N"], S["K"]), "bf16x3"))
+    # the vendor library on the same shapes, for comparison (not part of the surface):
+    # torch.matmul -> hipBLASLt; bf16 NN / NT / TN and the fp32 GEMM + bias (fp32 MFMA)
+    cases += [
+        ("vendor_hipblaslt_bf16_NN_8192x5120x1280", lambda: torch.matmul(A_mk, B_kn, out=C),
+         flop, "bf16"),
+        ("vendor_hipblaslt_bf16_NT_8192x5120x1280",
+         lambda: torch.matmul(A_mk, B_nk.t(), out=C), flop, "bf16"),
+        ("vendor_hipblaslt_bf16_TN_8192x5120x1280",
+         lambda: torch.matmul(A_km.t(), B_kn, out=C), flop, "bf16"),
+        ("vendor_hipblaslt_fp32_NN_4096^3_bias", lambda: torch.addmm(sbias, sa, sb, out=sc),
+         W.gemm_flop(S["M"], S["N"], S["K"]), "fp32_matrix"),
+    ]
     return cases
 
 

@@ -22,7 +22,7 @@
 // next product, O^T += V^T P^T (no LDS round trip of P). Q stays in registers (pre-scaled by
 // scale * log2 e, so the softmax uses the hardware exp2, split once); each K / V tile of 32 keys
 // is split while it is staged into LDS (K as [key][d], V transposed as [d][key]), with the next
-// tile's global loads in flight. 34 KB of LDS and <= 168 VGPRs per workgroup let 3 workgroups
+// tile's global loads in flight. 36 KB of LDS and <= 168 VGPRs per workgroup let 3 workgroups
 // share a CU, so the BASELINE grid (768 workgroups) runs in one round on 256 CUs. Causal
 // workgroups stop at the diagonal; their order is described at snake_item.
 #include <initializer_list>
@@ -46,14 +46,18 @@ constexpr int kBKV = 32;   // keys per K/V tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
-// LDS stage: K hi / K lo as [key][64 d] bf16 (128-byte rows, 16-byte chunk c of row r stored
-// at chunk c ^ ((r >> 1) & 7)), then V^T hi / V^T lo as [d][32 keys] bf16 with a 72-byte row
-// pitch. Both layouts make the fragment reads below conflict-free across 16 consecutive lanes.
-constexpr int kKBytes = kBKV * 128;                 // 4096
+// LDS stage: K hi / K lo as [key][64 d] bf16 with a 144-byte row pitch, then V^T hi / V^T lo
+// as [d][32 keys] bf16 with a 72-byte row pitch. gfx950's LDS serves 256 bytes per cycle over
+// 64 banks (16 lanes of a 16-byte read, 32 lanes of an 8-byte read): row c of K starts at
+// bank 36 c mod 64 and row d of V^T at 18 d mod 64, so the 16 (32) rows of one read cycle hit
+// distinct banks, and a lane's K fragments of the 4 k-steps sit at constant offsets from one
+// base address (immediate offsets, one address register).
+constexpr int kKPitch = 144;                        // bytes per K row
+constexpr int kKBytes = kBKV * kKPitch;             // 4608
 constexpr int kVtPitch = 72;                        // bytes per V^T row
 constexpr int kVtBytes = kHD * kVtPitch;            // 4608
-constexpr int kStageBytes = 2 * kKBytes + 2 * kVtBytes;  // 17408
-constexpr size_t kLdsBytes = 2 * kStageBytes;             // 34816, two stages
+constexpr int kStageBytes = 2 * kKBytes + 2 * kVtBytes;  // 18432
+constexpr size_t kLdsBytes = 2 * kStageBytes;             // 36864, two stages
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -146,8 +150,7 @@ struct KVLoader {
       const int key = 2 * pr + j;
       const u32x2_t s0 = split2(rk[j].x, rk[j].y), s1 = split2(rk[j].z, rk[j].w);
       const u32x2_t h = {s0.x, s1.x}, l = {s0.y, s1.y};
-      const int chunk = (d0 >> 3) ^ ((key >> 1) & 7);
-      const int off = key * 128 + chunk * 16 + (d0 & 7) * 2;
+      const int off = key * kKPitch + d0 * 2;
       *reinterpret_cast<u32x2_t*>(kh + off) = h;
       *reinterpret_cast<u32x2_t*>(kl + off) = l;
     }
@@ -238,8 +241,8 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
   const KVLoader ld(p.K + b * p.k_strideB + h * p.k_strideH,
                     p.V + b * p.v_strideB + h * p.v_strideH, p.k_strideM, p.v_strideM, T);
   f32x4_t rk[2], rv[2];
-  // per-lane LDS offsets: K fragment (key c, chunk 2 s + hh), V^T fragments (row 32 db + c)
-  const int kswz = (c >> 1) & 7;
+  // per-lane LDS offsets: K fragment (key c, d = 16 s + 8 hh), V^T fragments (row 32 db + c)
+  const int k_row = c * kKPitch + 16 * hh;
   const int vt_row = c * kVtPitch + 8 * hh;
   // a wave whose queries all precede key tile kt has nothing to add there (causal)
   auto active = [&](int kt) {
@@ -248,17 +251,28 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
   // Scores of a tile relative to the running reference m: the accumulator starts at -m (0
   // while this query has no reference yet), so the MFMAs deliver s - m directly.
   auto base_of = [&](float mm) { return mm == -INFINITY ? 0.f : -mm; };
+  // K fragments are read one k-step ahead of their MFMAs (the sched_group_barrier sequence
+  // keeps the compiler from sinking each read next to its use, which would expose the full LDS
+  // latency before every MFMA).
   auto qk = [&](const char* st, float c0) {
     f32x16_t sc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) sc[i] = c0;
+    bf16x8_t kh[4], kl[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const int off = c * 128 + (((2 * ks + hh) ^ kswz) * 16);
-      const bf16x8_t kh = as_bf16x8(*reinterpret_cast<const u32x4_t*>(st + off));
-      const bf16x8_t kl = as_bf16x8(*reinterpret_cast<const u32x4_t*>(st + kKBytes + off));
-      sc = mfma3(kh, kl, qh[ks], ql[ks], sc);
+      const int off = k_row + 32 * ks;
+      kh[ks] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(st + off));
+      kl[ks] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(st + kKBytes + off));
     }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) sc = mfma3(kh[ks], kl[ks], qh[ks], ql[ks], sc);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
     return sc;
   };
 
@@ -268,6 +282,24 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
   constexpr float kTau = 8.f;
   auto softmax_pv = [&](int kt, f32x16_t& sc, float c0, const char* st) {
     const int64_t k0 = static_cast<int64_t>(kt) * kBKV;
+    // V^T fragments (keys 16 ks + 4 hh .. + 3 and 16 ks + 8 + 4 hh .. + 3 of row d = 32 db + c,
+    // hi and lo) are read ahead of the exps, so that the exp / split work covers their LDS
+    // latency.
+    const char* vh = st + 2 * kKBytes;
+    const char* vl = vh + kVtBytes;
+    u32x4_t vfh[2][2], vfl[2][2];
+    auto vread = [&](int db) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int off = vt_row + 32 * db * kVtPitch + 32 * ks;
+        const u32x2_t a0 = *reinterpret_cast<const u32x2_t*>(vh + off);
+        const u32x2_t a1 = *reinterpret_cast<const u32x2_t*>(vh + off + 16);
+        const u32x2_t b0 = *reinterpret_cast<const u32x2_t*>(vl + off);
+        const u32x2_t b1 = *reinterpret_cast<const u32x2_t*>(vl + off + 16);
+        vfh[db][ks] = u32x4_t{a0.x, a0.y, a1.x, a1.y};
+        vfl[db][ks] = u32x4_t{b0.x, b0.y, b1.x, b1.y};
+      }
+    };
     // scores formed against an older reference are moved onto the current one
     const float cnow = base_of(m);
     if (__builtin_amdgcn_ballot_w64(c0 != cnow) != 0) {
@@ -320,6 +352,8 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
 #pragma unroll
       for (int db = 0; db < 2; ++db) o[db] *= alpha;
     }
+    vread(0);
+    vread(1);
     float ls = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -344,21 +378,15 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
       ph[ks] = as_bf16x8(u32x4_t{a0.x, a1.x, a2.x, a3.x});
       pl[ks] = as_bf16x8(u32x4_t{a0.y, a1.y, a2.y, a3.y});
     }
-    const char* vh = st + 2 * kKBytes;
-    const char* vl = vh + kVtBytes;
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        // keys 16 ks + 4 hh .. + 3 and 16 ks + 8 + 4 hh .. + 3 of row d = 32 db + c
-        const int off = vt_row + 32 * db * kVtPitch + 32 * ks;
-        const u32x2_t a0 = *reinterpret_cast<const u32x2_t*>(vh + off);
-        const u32x2_t a1 = *reinterpret_cast<const u32x2_t*>(vh + off + 16);
-        const u32x2_t b0 = *reinterpret_cast<const u32x2_t*>(vl + off);
-        const u32x2_t b1 = *reinterpret_cast<const u32x2_t*>(vl + off + 16);
-        o[db] = mfma3(as_bf16x8(u32x4_t{a0.x, a0.y, a1.x, a1.y}),
-                      as_bf16x8(u32x4_t{b0.x, b0.y, b1.x, b1.y}), ph[ks], pl[ks], o[db]);
-      }
+      for (int ks = 0; ks < 2; ++ks)
+        o[db] = mfma3(as_bf16x8(vfh[db][ks]), as_bf16x8(vfl[db][ks]), ph[ks], pl[ks], o[db]);
+    // V^T reads ahead of the exps, the exps ahead of the MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x400, 16, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);
   };
 
   // Two LDS stages: step kt forms and finishes tile kt from one stage while the global loads
