@@ -50,11 +50,11 @@ constexpr int kOffOh = kOffQl + kQPlane, kOffOl = kOffOh + kQPlane;  // dO
 constexpr int kOffSh = kOffOl + kQPlane, kOffSl = kOffSh + kKPlane;  // dS^T [key][query]
 constexpr int kOffL = kOffSl + kKPlane;
 constexpr int kOffD = kOffL + kBQ * 4;
-constexpr size_t kLdsBytes = kOffD + kBQ * 4;  // 131,584 bytes
-// The dQ key-half exchange reuses the Q / dO planes (4 blocks of 32 x 33 floats); the final
-// dK / dV exchange reuses the start of LDS (4 key groups x 2 x 32 x 65 floats).
-static_assert(4 * 32 * 33 * 4 <= 4 * kQPlane, "dQ exchange fits the Q / dO planes");
+constexpr int kOffPark = kOffD + kBQ * 4;      // dQ key-half exchange: 4 x 32 x 33 floats
+constexpr size_t kLdsBytes = kOffPark + 4 * 32 * 33 * 4;  // 148,480 bytes
+// The final dK / dV exchange reuses the start of LDS (4 key groups x 2 x 32 x 65 floats).
 static_assert(4 * 2 * 32 * 65 * 4 <= kLdsBytes, "dK / dV exchange fits");
+static_assert(kLdsBytes <= 160 * 1024, "fits gfx950's 160 KiB of LDS");
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -398,11 +398,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
       __builtin_amdgcn_sched_barrier(0);
     }
     // dq layout: query 32 qb + 8 (i/4) + 4 hh + i%4, d 32 dbq + c. Key half 1 parks its
-    // partial in the Q / dO planes (not read again this tile); key half 0 adds it and issues
-    // the atomics.
-    float HK_LDS* park = (float HK_LDS*)(lds + kOffQh) + (wave & 3) * (32 * 33);
+    // partial in the exchange area (read by key half 0 of the previous tile before the
+    // barrier at the top of this one); key half 0 adds it and issues the atomics.
+    float HK_LDS* park = (float HK_LDS*)(lds + kOffPark) + (wave & 3) * (32 * 33);
     float HK_LDS* pbase = park + 4 * hh * 33 + c;
-    __syncthreads();  // every wave is done reading the Q / dO planes
     if (kh == 1) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) pbase[(8 * (i >> 2) + (i & 3)) * 33] = dq[i];
