@@ -34,10 +34,15 @@ def _args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--suite", choices=["headline", "all", "copy"], default="all",
+    ap.add_argument("--suite", choices=["headline", "all", "copy", "compute"], default="all",
                     help="copy: only the plain-copy kernel used to calibrate rocprofv3's "
-                         "FETCH_SIZE / WRITE_SIZE counters (prints its byte count)")
+                         "FETCH_SIZE / WRITE_SIZE counters (prints its byte count); compute: "
+                         "only the MFMA kernels (GEMMs, attention) of the per-kernel suite, for "
+                         "counter runs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cases", default="",
+                    help="with --suite compute: comma-separated names of the cases to run "
+                         "(default: all)")
     ap.add_argument("--reps", type=int, default=20, help="repetitions per per-kernel timing")
     return ap.parse_args()
 
@@ -238,10 +243,19 @@ def run_cpu_baseline():
 # ------------------------------------------------------------------------------------------------
 # per-kernel suite
 # ------------------------------------------------------------------------------------------------
-def per_kernel_suite(flush):
+def per_kernel_suite(flush, compute_only=False):
     out = {}
     g = torch.Generator(device=DEV)
     g.manual_seed(99)
+    if compute_only:
+        cases = gemm_cases(g) + attention_cases(g)
+        if ARGS.cases:
+            keep = set(ARGS.cases.split(","))
+            unknown = keep - {c[0] for c in cases}
+            if unknown:
+                raise SystemExit(f"bench.py: unknown case(s) {sorted(unknown)}")
+            cases = [c for c in cases if c[0] in keep]
+        return time_cases(cases, flush, out)
     # LayerNorm configs[0], in fp32 and in bf16 / fp16 storage (fp32 statistics); gamma and
     # beta are shared by the buffer sets
     R, C = W.LN["rows"], W.LN["cols"]
@@ -289,6 +303,11 @@ def per_kernel_suite(flush):
     cases += gemm_cases(g)
     cases += gemv_cases(g)
     cases += attention_cases(g)
+    return time_cases(cases, flush, out)
+
+
+def time_cases(cases, flush, out):
+    """Times each (name, fn or [fns], work, bound) case; fills and returns `out`."""
     for name, fn, work, bound in cases:
         fns = fn if isinstance(fn, list) else [fn] * (1 if bound == "hbm" else COMPUTE_BURST)
         t = time_burst(fns, ARGS.reps, flush)
@@ -455,6 +474,10 @@ def main():
     log(f"device: {torch.cuda.get_device_name(0)}")
     if ARGS.suite == "copy":
         run_copy_calibration()
+        return
+    if ARGS.suite == "compute":
+        print(json.dumps({"per_kernel": per_kernel_suite(Flusher(), compute_only=True)}),
+              flush=True)
         return
     ks, step_bytes, ms_step, per = run_headline()
     value = step_bytes / (ms_step * 1e-3) / 1e9

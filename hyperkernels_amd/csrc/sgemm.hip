@@ -1,4 +1,5 @@
-// sgemm.hip - batched FP32 GEMM on gfx950 fp32 MFMA with split-K and a fused bias epilogue.
+// sgemm.hip - batched FP32 GEMM on gfx950 (bf16x3 split or fp32 MFMA) with split-K and a fused
+// bias epilogue.
 //
 // Reference behaviour:
 //   sgemm_sm89_kernel<Cfg, Aligned, SplitK, Layout>   blas/fp32/sgemm_sm89_core_template.cu:85-327

@@ -10,6 +10,15 @@ Usage (after `rocprofv3 ... --output-format csv -d DIR -- python3 bench.py ...`)
         each scaled by the factor that makes the same counter read COPY_BYTES for a plain copy
         kernel (torch's elementwise `mul(src, 1, out=dst)` over COPY_BYTES of float32).
 
+    python -m hyperkernels_amd.rocprof_summary pmc FILTER DIR [DIR ...]
+        per kernel whose symbol contains FILTER: dispatches, mean duration and mean value per
+        dispatch of every counter found in the `--pmc` runs DIR..., plus derived figures:
+          clock_ghz  = GRBM_GUI_ACTIVE / Num_Xcc / duration (GRBM_GUI_ACTIVE is summed over
+                       the XCDs; the agent's Num_Xcc and Simd_Count come from *_agent_info.csv);
+          mfma_busy  = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / Num_Xcc * Simd_Count), the
+                       fraction of SIMD cycles in which the matrix core is busy;
+          lds_conflict = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE.
+
 The traffic lines (`traffic: <name> fetch_bytes=... write_bytes=... traffic_bytes=...`) are what
 bench.py reads back for the `roofline.traffic` field of its dominant kernel.
 """
@@ -118,11 +127,59 @@ def read_traffic(path):
     return out
 
 
+def _agent(d):
+    """(Num_Xcc, Simd_Count) of the GPU agent of a rocprofv3 output directory."""
+    for r in _csvs(d, "agent_info.csv"):
+        if r.get("Agent_Type") == "GPU":
+            return int(r["Num_Xcc"]), int(r["Simd_Count"])
+    raise SystemExit(f"no GPU agent in {d}")
+
+
+def pmc(filt, dirs):
+    """Per-kernel mean counters per dispatch over several `--pmc` runs (one counter set each)."""
+    vals = defaultdict(lambda: defaultdict(list))
+    durs = defaultdict(list)
+    xcc, simds = _agent(dirs[0])
+    for d in dirs:
+        per = defaultdict(lambda: defaultdict(float))
+        span = {}
+        for r in _csvs(d, "counter_collection.csv"):
+            if filt not in r["Kernel_Name"]:
+                continue
+            key = (r["Kernel_Name"], r.get("Process_Id", ""), r["Dispatch_Id"])
+            per[key][r["Counter_Name"]] += float(r["Counter_Value"])
+            span[key] = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+        for key, cs in per.items():
+            for c, v in cs.items():
+                vals[key[0]][c].append(v)
+            durs[key[0]].append(span[key])
+    lines = []
+    for name in sorted(vals, key=lambda n: -sum(durs[n]) / len(durs[n])):
+        cs = {c: sum(v) / len(v) for c, v in vals[name].items()}
+        dur = sum(durs[name]) / len(durs[name])
+        lines.append(f"kernel {_short(name)}: dispatches/run {len(durs[name]) // len(dirs)}, "
+                     f"mean duration {dur / 1e3:.1f} us")
+        for c in sorted(cs):
+            lines.append(f"  {c:30s} {cs[c]:18,.0f}")
+        if "GRBM_GUI_ACTIVE" in cs:
+            cyc = cs["GRBM_GUI_ACTIVE"] / xcc
+            lines.append(f"  {'clock_ghz':30s} {cyc / dur:18.3f}")
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in cs:
+                lines.append(f"  {'mfma_busy':30s} "
+                             f"{cs['SQ_VALU_MFMA_BUSY_CYCLES'] / (cyc * simds):18.3f}")
+        if cs.get("SQ_LDS_IDX_ACTIVE"):
+            lines.append(f"  {'lds_conflict':30s} "
+                         f"{cs.get('SQ_LDS_BANK_CONFLICT', 0.0) / cs['SQ_LDS_IDX_ACTIVE']:18.3f}")
+    return lines
+
+
 def main(argv):
     if argv[:1] == ["stats"]:
         print(f"{'kernel':90s} {'calls':>6s} {'avg_us':>10s} {'min_us':>10s} {'max_us':>10s} {'pct':>6s}")
         for n, c, a, lo, hi, pct in kernel_stats(argv[1]):
             print(f"{_short(n):90s} {c:6d} {a / 1e3:10.2f} {lo / 1e3:10.2f} {hi / 1e3:10.2f} {pct:6.2f}")
+    elif argv[:1] == ["pmc"] and len(argv) >= 3:
+        print("\n".join(pmc(argv[1], argv[2:])))
     elif argv[:1] == ["traffic"]:
         print("\n".join(traffic(argv[1], argv[2], argv[3], argv[4], float(argv[5]))))
     else:

@@ -352,7 +352,9 @@ HK_API hipError_t hk_bgemm_core_bias(int layout, int splitK, int M, int N, int K
                                      long long strideC, int batchCount, hipStream_t stream);
 
 /* ------------------------------------------------------------------------------------------
- * FP32 batched GEMM on fp32 MFMA (full fp32 products; the reference uses single-pass TF32),
+ * FP32 batched GEMM with fp32-class products (the reference uses single-pass TF32; gfx950 has no
+ * TF32 MFMA): a bf16x3 split on the bf16 MFMA (x = hi + lo, a b = ah bh + ah bl + al bh, relative
+ * error ~1e-5) when every dimension is a multiple of 8, exact fp32 MFMA products otherwise,
  * row-major, layout HK_LAYOUT_{NT,TN,NN} as SgemmLayout (blas/fp32/sgemm_sm89_core_template.cu:9).
  * hk_sgemm replaces sgemm_sm89_kernel<Cfg, Aligned, SplitK, Layout> (…core_template.cu:85-94):
  *   C = alpha * op(A) op(B) + beta * C + bias, the bias added EXACTLY ONCE whatever splitK is
@@ -388,7 +390,8 @@ HK_API hipError_t hk_sgemm_layout(int layout, int M, int N, int K, float alpha, 
                                   hipStream_t stream);
 
 /* ------------------------------------------------------------------------------------------
- * Attention, fp32 I/O, head_dim 64 (the reference's only instantiation), fp32 MFMA.
+ * Attention, fp32 I/O, head_dim 64 (the reference's only instantiation), products as a bf16x3
+ * split on the bf16 MFMA (fp32-class accuracy, relative error ~1e-5; gfx950 has no TF32 MFMA).
  * Tensors are [B, nh, T, head_dim] with arbitrary batch/head/row strides (elements; last-dim
  * stride 1; strides multiples of 4 and 16-byte aligned bases), LSE and D are [B, nh, T].
  * The parameter blocks repeat the reference's field order and types exactly:
