@@ -350,6 +350,19 @@ def attention_cases(g):
                       lambda c=causal, lse=lse, Dt=Dt, dq=dq, dk=dk, dv=dv: hk.attn_backward(
                           q, k, v, do, lse, Dt, c, dq=dq, dk=dk, dv=dv),
                       W.attn_bwd_flop(B, H, T, D, causal), "bf16x3"))
+    # the vendor path on the same tensors, for comparison (not part of the surface): torch's
+    # scaled_dot_product_attention in fp32 on its memory-efficient backend (AOTriton)
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    def sdpa(c):
+        with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION]):
+            F.scaled_dot_product_attention(q, k, v, is_causal=c)
+    for causal in (True, False):
+        tag = "causal" if causal else "noncausal"
+        cases.append((f"vendor_torch_sdpa_fp32_fwd_{tag}_8x12x1024x64",
+                      lambda c=causal: sdpa(c), W.attn_fwd_flop(B, H, T, D, causal),
+                      "fp32_matrix"))
     return cases
 
 

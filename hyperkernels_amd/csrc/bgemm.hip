@@ -417,17 +417,20 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
 }
 
 // C = alpha * sum_s part[s] + beta * C (split order), fp32 -> bf16.
+// I: the index type, uint32_t when every index of the launch fits in 31 bits (a 64-bit
+// division costs several times a 32-bit one).
+template <typename I>
 __global__ __launch_bounds__(256) void bgemm_splitk_finalize(const float* __restrict__ part,
                                                              int split_k, int batch, int M, int N,
                                                              Epi ep, uint16_t* __restrict__ C,
                                                              int64_t ldc, int64_t sC) {
   // 4 consecutive outputs per thread (N is a multiple of 8 on the tiled path)
-  const int64_t idx = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
-  const int64_t mn = static_cast<int64_t>(M) * N;
+  const I idx = (static_cast<I>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  const I mn = static_cast<I>(M) * N;
   if (idx >= mn * batch) return;
-  const int b = static_cast<int>(idx / mn);
-  const int64_t e = idx - b * mn;
-  const int row = static_cast<int>(e / N), col = static_cast<int>(e - static_cast<int64_t>(row) * N);
+  const I b = idx / mn;
+  const I e = idx - b * mn;
+  const int row = static_cast<int>(e / N), col = static_cast<int>(e - static_cast<I>(row) * N);
   f32x2_t lo = f32x2_t{0.f, 0.f}, hi = f32x2_t{0.f, 0.f};
   for (int k = 0; k < split_k; ++k) {
     const float4 v = *reinterpret_cast<const float4*>(part + (static_cast<int64_t>(k) * batch + b) * mn + e);
@@ -618,9 +621,15 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
   HK_RETURN_IF_ERROR(dispatch_layout<true>(ta, tb, grid, stream, M, N, K, ep, A, lda, strideA,
                                            B, ldb, strideB, C, ldc, strideC, used, kps, part));
   const int64_t total = static_cast<int64_t>(M) * N * batchCount;
-  hipLaunchKernelGGL(bgemm_splitk_finalize, dim3(static_cast<unsigned>(hk::ceil_div(total, 1024))),
-                     dim3(256), 0, stream, part, used, batchCount, M, N, ep, C,
-                     static_cast<int64_t>(ldc), static_cast<int64_t>(strideC));
+  const dim3 fgrid(static_cast<unsigned>(hk::ceil_div(total, 1024)));
+  if (total < (int64_t{1} << 31))
+    hipLaunchKernelGGL(bgemm_splitk_finalize<uint32_t>, fgrid, dim3(256), 0, stream, part, used,
+                       batchCount, M, N, ep, C, static_cast<int64_t>(ldc),
+                       static_cast<int64_t>(strideC));
+  else
+    hipLaunchKernelGGL(bgemm_splitk_finalize<int64_t>, fgrid, dim3(256), 0, stream, part, used,
+                       batchCount, M, N, ep, C, static_cast<int64_t>(ldc),
+                       static_cast<int64_t>(strideC));
   return hk::launch_status();
 }
 
