@@ -19,32 +19,37 @@
 
 namespace {
 
-constexpr float kSqrt2OverPi = 0.7978845608028654f;  // sqrt(2/pi)
-constexpr float kGeluCoef = 0.044715f;               // Hendrycks & Gimpel tanh fit
 constexpr int kThreads = 256;
 constexpr int kUnroll = 1;
 
-// (1 + tanh(u)) / 2 = sigmoid(2u) = 1 / (1 + exp(-2u)): no cancellation for u << 0, where
-// 1 + tanh(u) formed from a rounded tanh loses most of its digits. exp overflow (u << 0) gives
-// s = 0 and exp underflow (u >> 0) gives s = 1, the correct limits.
-__device__ __forceinline__ float half_one_plus_tanh(float u) {
-  return __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * u));
+// With u = c (x + a x^3) (c = sqrt(2/pi), a = 0.044715, the Hendrycks & Gimpel tanh fit):
+// (1 + tanh(u)) / 2 = sigmoid(2u) = 1 / (1 + 2^(-2 log2(e) u)): no cancellation for u << 0,
+// where 1 + tanh(u) formed from a rounded tanh loses most of its digits. The exponent is
+// -2 log2(e) u = x (k1 + k2 x^2) with the constants folded (float64-rounded once):
+//   k1 = -2 log2(e) c, k2 = k1 a.
+// 2^t overflow (x << 0) gives s = 0 and underflow (x >> 0) gives s = 1, the correct limits.
+// v_exp_f32 is the hardware 2^t (about 1 ulp) and v_rcp_f32 the hardware reciprocal (1 ulp):
+// s carries a few ulp of relative error everywhere.
+constexpr float kK1 = -2.302208198144325f;   // -2 log2(e) sqrt(2/pi)
+constexpr float kK2 = -0.1029432395800235f;  // kK1 * 0.044715
+constexpr float kC = 0.7978845608028654f;    // sqrt(2/pi)
+constexpr float kC3a = 0.10703222440890f;    // 3 * 0.044715 * sqrt(2/pi)
+
+__device__ __forceinline__ float sigmoid_2u(float x, float x2) {
+  const float t = x * __builtin_fmaf(kK2, x2, kK1);
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
 // GELU(x) = 0.5 x (1 + tanh(u)) = x s
-__device__ __forceinline__ float gelu_fwd(float x) {
-  const float u = kSqrt2OverPi * (x + kGeluCoef * x * x * x);
-  return x * half_one_plus_tanh(u);
-}
+__device__ __forceinline__ float gelu_fwd(float x) { return x * sigmoid_2u(x, x * x); }
 
-// GELU'(x) = 0.5 (1 + th) + 0.5 x (1 - th^2) du = s + 2 x s (1 - s) du, with s as above
-// (1 - th^2 = (1 - th)(1 + th) = 4 s (1 - s)).
+// GELU'(x) = 0.5 (1 + th) + 0.5 x (1 - th^2) du = s + 2 x du s (1 - s), with s as above,
+// 1 - th^2 = (1 - th)(1 + th) = 4 s (1 - s) and du = c (1 + 3 a x^2).
 __device__ __forceinline__ float gelu_grad(float x) {
   const float x2 = x * x;
-  const float u = kSqrt2OverPi * (x + kGeluCoef * x2 * x);
-  const float du = kSqrt2OverPi * (1.0f + 3.0f * kGeluCoef * x2);
-  const float s = half_one_plus_tanh(u);
-  return s + 2.0f * x * (s * (1.0f - s)) * du;
+  const float s = sigmoid_2u(x, x2);
+  const float two_x_du = 2.0f * x * __builtin_fmaf(kC3a, x2, kC);
+  return __builtin_fmaf(two_x_du, __builtin_fmaf(-s, s, s), s);
 }
 
 // Vector body: nvec 16-byte vectors, all pointers 16-byte aligned.

@@ -13,20 +13,21 @@
 namespace hk {
 
 // ---- bf16 <-> fp32 -------------------------------------------------------------------------
-// bf16 is the upper half of an fp32 bit pattern. Rounding is round-to-nearest-even; NaNs stay
-// NaN (quiet bit forced), matching __float2bfloat16_rn semantics.
+// bf16 is the upper half of an fp32 bit pattern. fp32 -> bf16 is gfx950's v_cvt_pk_bf16_f32:
+// round to nearest even (denormals kept), NaN stays NaN, matching __float2bfloat16_rn on every
+// non-NaN value; one instruction converts two values.
+typedef float hk_f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 hk_bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
-}
 // Two fp32 -> packed bf16x2 (lo in bits 0..15).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_convertvector(hk_f32x2_t{lo, hi}, hk_bf16x2_t));
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 // ---- fp16 <-> fp32 -------------------------------------------------------------------------
@@ -95,7 +96,11 @@ struct Half16 {
     }
   }
   __device__ static uint32_t pack2(float lo, float hi) {
-    return static_cast<uint32_t>(FromF32(lo)) | (static_cast<uint32_t>(FromF32(hi)) << 16);
+    if constexpr (FromF32 == f32_to_bf16) {
+      return pack_bf16x2(lo, hi);  // one v_cvt_pk_bf16_f32 for the pair
+    } else {
+      return static_cast<uint32_t>(FromF32(lo)) | (static_cast<uint32_t>(FromF32(hi)) << 16);
+    }
   }
   __device__ static uint4 pack(const float* f) {
     return make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
