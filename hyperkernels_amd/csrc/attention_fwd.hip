@@ -58,6 +58,12 @@ constexpr int kVtPitch = 72;                        // bytes per V^T row
 constexpr int kVtBytes = kHD * kVtPitch;            // 4608
 constexpr int kStageBytes = 2 * kKBytes + 2 * kVtBytes;  // 18432
 constexpr size_t kLdsBytes = 2 * kStageBytes;             // 36864, two stages
+// Dropout: each wave's 32 x 32 block of mask factors passes through a wave-private LDS area
+// (32 rows, 144-byte pitch: row r starts at bank 36 r mod 64), written as coalesced 128-byte
+// row segments and read back as the lane's 16 factors.
+constexpr int kMaskPitch = 144;
+constexpr int kMaskWaveBytes = 32 * kMaskPitch;           // 4608
+constexpr size_t kLdsBytesDrop = kLdsBytes + 4 * kMaskWaveBytes;  // 55296
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -280,7 +286,49 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
   // scores exceed it by more than kTau or on the query's first tile, so exp2(s - m) <= 2^kTau
   // and most tiles need neither a subtraction per score nor a rescale of O.
   constexpr float kTau = 8.f;
-  auto softmax_pv = [&](int kt, f32x16_t& sc, float c0, const char* st) {
+  // Dropout factors of key tile kt. mvec (16-byte rows): coalesced, lane L loads part g = row
+  // q0w + 8 g + L / 8, keys k0 + 4 (L % 8) .. + 3 (8 lanes per 128-byte row segment), and
+  // mask_to_lanes redistributes them through LDS. Otherwise: the lane's own 16 factors (query q,
+  // keys k0 + 8 g + 4 hh .. + 3), element by element.
+  auto load_mask = [&](int kt, float4 (&mk)[4]) {
+    const int64_t k0 = static_cast<int64_t>(kt) * kBKV;
+    if (mvec) {
+      const int64_t key = k0 + 4 * (lane & 7);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t r = q0w + 8 * g + (lane >> 3);
+        mk[g] = r < T && key < T ? *reinterpret_cast<const float4*>(
+                                       p.dropout_mask + (static_cast<int64_t>(bh) * T + r) * T + key)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      return;
+    }
+    const float* mrow = p.dropout_mask + (static_cast<int64_t>(bh) * T + q) * T;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int64_t key = k0 + 8 * g + 4 * hh;
+      const bool ok = q < T;
+      mk[g].x = ok && key + 0 < T ? mrow[key + 0] : 0.f;
+      mk[g].y = ok && key + 1 < T ? mrow[key + 1] : 0.f;
+      mk[g].z = ok && key + 2 < T ? mrow[key + 2] : 0.f;
+      mk[g].w = ok && key + 3 < T ? mrow[key + 3] : 0.f;
+    }
+  };
+  // mvec: the coalesced parts -> this lane's factors (query c, keys 8 g + 4 hh .. + 3). The
+  // wave's LDS area is reused every tile; a wave's LDS operations complete in order, so the
+  // reads of one tile precede the writes of the next.
+  auto mask_to_lanes = [&](float4 (&mk)[4]) {
+    if (!mvec) return;
+    char* reg = lds + kLdsBytes + wave * kMaskWaveBytes;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *reinterpret_cast<float4*>(reg + (8 * g + (lane >> 3)) * kMaskPitch + 16 * (lane & 7)) =
+          mk[g];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      mk[g] = *reinterpret_cast<const float4*>(reg + c * kMaskPitch + (8 * g + 4 * hh) * 4);
+  };
+  auto softmax_pv = [&](int kt, f32x16_t& sc, float c0, const char* st, const float4 (&mk)[4]) {
     const int64_t k0 = static_cast<int64_t>(kt) * kBKV;
     // V^T fragments (keys 16 ks + 4 hh .. + 3 and 16 ks + 8 + 4 hh .. + 3 of row d = 32 db + c,
     // hi and lo) are read ahead of the exps, so that the exp / split work covers their LDS
@@ -305,25 +353,6 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
     if (__builtin_amdgcn_ballot_w64(c0 != cnow) != 0) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) sc[i] += cnow - c0;
-    }
-    // dropout factors of this lane's 16 scores
-    float4 mk[4];
-    if (DROP) {
-      const float* mrow = p.dropout_mask + (static_cast<int64_t>(bh) * T + q) * T;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int64_t key = k0 + 8 * g + 4 * hh;
-        if (q < T && mvec) {
-          mk[g] = key < T ? *reinterpret_cast<const float4*>(mrow + key)
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
-        } else {
-          const bool ok = q < T;
-          mk[g].x = ok && key + 0 < T ? mrow[key + 0] : 0.f;
-          mk[g].y = ok && key + 1 < T ? mrow[key + 1] : 0.f;
-          mk[g].z = ok && key + 2 < T ? mrow[key + 2] : 0.f;
-          mk[g].w = ok && key + 3 < T ? mrow[key + 3] : 0.f;
-        }
-      }
     }
     // mask (causal: key > query; any: key >= T)
     const bool need_mask = (p.is_causal && k0 + kBKV - 1 > q0w) || k0 + kBKV > T;
@@ -396,15 +425,26 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
     KVLoader::store(lds, rk, rv);
   }
   __syncthreads();
+  // dropout: the mask factors of tile kt + 1 are loaded while tile
+  // kt is computed
+  float4 mk_next[4];
+  if (DROP && nkv > 0 && active(0)) load_mask(0, mk_next);
   for (int kt = 0; kt < nkv; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < nkv;
     if (more) ld.load(static_cast<int64_t>(kt + 1) * kBKV, rk, rv);
+    float4 mk[4];
+    if (DROP) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) mk[g] = mk_next[g];
+      if (more && active(kt + 1)) load_mask(kt + 1, mk_next);
+      if (active(kt)) mask_to_lanes(mk);
+    }
     const char* st = lds + cur * kStageBytes;
     if (active(kt)) {
       const float c0 = base_of(m);
       f32x16_t sc = qk(st, c0);
-      softmax_pv(kt, sc, c0, st);
+      softmax_pv(kt, sc, c0, st, mk);
     }
     if (more) KVLoader::store(lds + (cur ^ 1) * kStageBytes, rk, rv);
     __syncthreads();
@@ -495,16 +535,18 @@ extern "C" hipError_t hk_fused_attn_forward(const hk_attn_fwd_params* params, in
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
-    for (const void* k : {reinterpret_cast<const void*>(&attn_fwd_kernel<false>),
-                          reinterpret_cast<const void*>(&attn_fwd_kernel<true>)}) {
+    for (int d = 0; d < 2; ++d) {
+      const void* k = d ? reinterpret_cast<const void*>(&attn_fwd_kernel<true>)
+                        : reinterpret_cast<const void*>(&attn_fwd_kernel<false>);
       const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               static_cast<int>(kLdsBytes));
+                                               static_cast<int>(d ? kLdsBytesDrop : kLdsBytes));
       if (e != hipSuccess) attr = e;
     }
   });
   HK_RETURN_IF_ERROR(attr);
   hipLaunchKernelGGL(drop ? attn_fwd_kernel<true> : attn_fwd_kernel<false>,
-                     dim3(static_cast<unsigned>(nqt * bh)), dim3(256), kLdsBytes, stream, p,
+                     dim3(static_cast<unsigned>(nqt * bh)), dim3(256),
+                     drop ? kLdsBytesDrop : kLdsBytes, stream, p,
                      static_cast<int>(bh), hk::device_cu_count(), mvec);
   return hk::launch_status();
 }
