@@ -181,6 +181,15 @@ __device__ __forceinline__ float bias_at(const Epi& ep, int row, int col) {
   return hk::bf16_to_f32(ep.bias[row * ep.brow + col * ep.bcol]);
 }
 
+// Bias element of column col of batch b for an fp32 output (hk::F32Out).
+__device__ __forceinline__ float f32out_bias(const hk::F32Out& fo, int M, int N, int b, int col) {
+  if (fo.bias_stride == N) return fo.bias[col];
+  if (fo.bias_stride == static_cast<int64_t>(M) * N)
+    return fo.bias[static_cast<int64_t>(b % M) * N + col];
+  if (fo.bias_stride == 1) return fo.bias[0];
+  return 0.f;
+}
+
 // Scheduling hint: NR LDS reads spread over NM MFMAs (reads first in each pair), so the
 // operands of the next k step are fetched while the current one multiplies.
 template <int NM, int NR, int Q = 0>
@@ -245,7 +254,8 @@ template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL>
 __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
     int M, int N, int K, Epi ep, const uint16_t* __restrict__ A, int64_t lda, int64_t sA,
     const uint16_t* __restrict__ B, int64_t ldb, int64_t sB, uint16_t* __restrict__ C,
-    int64_t ldc, int64_t sC, int split_k, int k_per_split, float* __restrict__ part) {
+    int64_t ldc, int64_t sC, int split_k, int k_per_split, float* __restrict__ part,
+    hk::F32Out fo) {
   using OA = TileOperand<A_KMAJOR>;
   using OB = TileOperand<B_KMAJOR>;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
@@ -394,6 +404,37 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
   // wm*128 + 32 i + l % 32 and columns wn*128 + 32 j + 8 q + 4 (l / 32) .. +3.
   const int row0 = m0 + wm * kWaveM + (lane & 31);
   const int col0 = n0 + wn * kWaveN + 4 * (lane >> 5);
+  if (PARTIAL && fo.C) {
+    // one split: fp32 C with alpha, beta and the bias applied here
+    float* cb = fo.C + static_cast<int64_t>(batch) * fo.sC;
+#pragma unroll
+    for (int i = 0; i < kBlkM; ++i) {
+      const int row = row0 + 32 * i;
+      if (row >= M) continue;
+#pragma unroll
+      for (int j = 0; j < kBlkN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int col = col0 + 32 * j + 8 * q;
+          if (col >= N) continue;
+          float4* dst = reinterpret_cast<float4*>(cb + static_cast<int64_t>(row) * fo.ldc + col);
+          float4 v = make_float4(fo.alpha * acc[i][j][4 * q], fo.alpha * acc[i][j][4 * q + 1],
+                                 fo.alpha * acc[i][j][4 * q + 2], fo.alpha * acc[i][j][4 * q + 3]);
+          if (fo.beta != 0.0f) {
+            const float4 o = *dst;
+            v.x += fo.beta * o.x; v.y += fo.beta * o.y; v.z += fo.beta * o.z; v.w += fo.beta * o.w;
+          }
+          if (fo.bias) {
+            v.x += fo.bias_scale * f32out_bias(fo, M, N, batch, col);
+            v.y += fo.bias_scale * f32out_bias(fo, M, N, batch, col + 1);
+            v.z += fo.bias_scale * f32out_bias(fo, M, N, batch, col + 2);
+            v.w += fo.bias_scale * f32out_bias(fo, M, N, batch, col + 3);
+          }
+          *dst = v;
+        }
+    }
+    return;
+  }
   if (PARTIAL) {
     float* out = part + (static_cast<int64_t>(split) * (gridDim.z / split_k) + batch) *
                             static_cast<int64_t>(M) * N;
@@ -501,7 +542,8 @@ template <bool AK, bool BKM, bool P>
 hipError_t launch_tiled(dim3 grid, hipStream_t stream, int M, int N, int K, const Epi& ep,
                         const uint16_t* A, int64_t lda, int64_t sA, const uint16_t* B,
                         int64_t ldb, int64_t sB, uint16_t* C, int64_t ldc,
-                        int64_t sC, int split_k, int kps, float* part) {
+                        int64_t sC, int split_k, int kps, float* part,
+                        const hk::F32Out& fo = hk::F32Out{}) {
   static std::once_flag once;
   static hipError_t attr_status = hipSuccess;
   std::call_once(once, [] {
@@ -511,7 +553,7 @@ hipError_t launch_tiled(dim3 grid, hipStream_t stream, int M, int N, int K, cons
   });
   HK_RETURN_IF_ERROR(attr_status);
   hipLaunchKernelGGL((bgemm_tiled<AK, BKM, P>), grid, dim3(kThreads), kLdsBytes, stream, M, N, K,
-                     ep, A, lda, sA, B, ldb, sB, C, ldc, sC, split_k, kps, part);
+                     ep, A, lda, sA, B, ldb, sB, C, ldc, sC, split_k, kps, part, fo);
   return hk::launch_status();
 }
 
@@ -519,19 +561,20 @@ template <bool P>
 hipError_t dispatch_layout(bool ta, bool tb, dim3 grid, hipStream_t stream, int M, int N, int K,
                            const Epi& ep, const uint16_t* A, int64_t lda, int64_t sA,
                            const uint16_t* B, int64_t ldb, int64_t sB, uint16_t* C,
-                           int64_t ldc, int64_t sC, int split_k, int kps, float* part) {
+                           int64_t ldc, int64_t sC, int split_k, int kps, float* part,
+                           const hk::F32Out& fo = hk::F32Out{}) {
   // A is k-major unless transposed; B is k-major only when transposed.
   if (!ta && !tb)
     return launch_tiled<true, false, P>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
-                                        C, ldc, sC, split_k, kps, part);
+                                        C, ldc, sC, split_k, kps, part, fo);
   if (!ta && tb)
     return launch_tiled<true, true, P>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
-                                       C, ldc, sC, split_k, kps, part);
+                                       C, ldc, sC, split_k, kps, part, fo);
   if (ta && !tb)
     return launch_tiled<false, false, P>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
-                                         C, ldc, sC, split_k, kps, part);
+                                         C, ldc, sC, split_k, kps, part, fo);
   return launch_tiled<false, true, P>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
-                                      C, ldc, sC, split_k, kps, part);
+                                      C, ldc, sC, split_k, kps, part, fo);
 }
 
 // Split-K chosen by the library when the caller gives none: the split that minimises a simple
@@ -651,7 +694,8 @@ void bgemm_split_plan(int M, int N, int K, int batch, int* used, int* kps) {
 
 hipError_t bgemm_partials(bool ta, bool tb, int M, int N, int K, const hk_bf16* A, int64_t lda,
                           int64_t sA, const hk_bf16* B, int64_t ldb, int64_t sB, int batch,
-                          int used, int kps, float* part, hipStream_t stream) {
+                          int used, int kps, float* part, const F32Out* out,
+                          hipStream_t stream) {
   const int contig_a = ta ? M : K, contig_b = tb ? K : N;
   HK_CHECK_ARG(M > 0 && N > 0 && K > 0 && batch > 0 && used >= 1 && kps % BK == 0);
   HK_CHECK_ARG(contig_a % 8 == 0 && contig_b % 8 == 0 && N % 8 == 0 && lda % 8 == 0 &&
@@ -661,8 +705,9 @@ hipError_t bgemm_partials(bool ta, bool tb, int M, int N, int K, const hk_bf16* 
   HK_CHECK_ARG(tiles <= INT32_MAX && static_cast<int64_t>(batch) * used <= 65535);
   const Epi ep{1.0f, 0.0f, nullptr, 0, 0};
   dim3 grid(static_cast<unsigned>(tiles), 1, batch * used);
+  const F32Out fo = used == 1 && out ? *out : F32Out{};
   return dispatch_layout<true>(ta, tb, grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB, nullptr,
-                               0, 0, used, kps, part);
+                               0, 0, used, kps, part, fo);
 }
 
 }  // namespace hk

@@ -40,14 +40,29 @@ hipError_t bgemv_run(bool dot_form, int R, int K, hk_bf16 alpha, hk_bf16 beta,
                      int64_t sx, hk_bf16* y, int64_t incy, int64_t sy, int batch,
                      hipStream_t stream);
 
+// fp32 output written straight from the BF16 GEMM tiles when the product has one split:
+// C[b][row][col] = alpha * acc + beta * C (C not read when beta == 0) + bias_scale * bias, the
+// bias selected by bias_stride as hk_sgemm does (N: bias[col]; M*N: bias[(b % M) * N + col];
+// 1: bias[0]; bias NULL: none).
+struct F32Out {
+  float* C;
+  int64_t ldc, sC;
+  float alpha, beta;
+  const float* bias;
+  int64_t bias_stride;
+  float bias_scale;
+};
+
 // fp32 product of bf16 operands on the BF16 GEMM tiles (bgemm.hip), written as split-K partials
 // part[s][batch][M][N] (s < used) of op(A) op(B) over k-range [s kps, (s + 1) kps); their sum
-// in split order is the product. Needs the tiled path's alignment: 8-element multiples and
-// 16-byte aligned bases. bgemm_split_plan picks (used, kps) for a shape.
+// in split order is the product. With used == 1 and out != NULL the tiles write out->C through
+// its epilogue instead (part is not touched). Needs the tiled path's alignment: 8-element
+// multiples and 16-byte aligned bases. bgemm_split_plan picks (used, kps) for a shape.
 void bgemm_split_plan(int M, int N, int K, int batch, int* used, int* kps);
 hipError_t bgemm_partials(bool ta, bool tb, int M, int N, int K, const hk_bf16* A, int64_t lda,
                           int64_t sA, const hk_bf16* B, int64_t ldb, int64_t sB, int batch,
-                          int used, int kps, float* part, hipStream_t stream);
+                          int used, int kps, float* part, const F32Out* out,
+                          hipStream_t stream);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }

@@ -15,10 +15,11 @@
 // Two paths:
 //   bf16x3 (shapes whose dimensions are multiples of 8, the common case): A and B are split into
 //     bf16 hi / lo operands over a tripled k axis (split3) so that one bf16 GEMM on the BF16 GEMM
-//     tiles of this library (bgemm.hip) sums ah bh + ah bl + al bh in fp32; the split-K
-//     finalize below applies alpha, beta and the bias. Relative error ~1e-5 (max-rel 3e-6 at
-//     4096^3 against a float64 product) at bf16 MFMA rate: 4096^3 + bias in ~0.57 ms against
-//     ~1.17 ms on the fp32 MFMA. Roofline: the bf16 peak / 3 (three products per fp32 product).
+//     tiles of this library (bgemm.hip) sums ah bh + ah bl + al bh in fp32. With one k split
+//     the GEMM tiles apply alpha, beta and the bias and write C; with more, the split-K
+//     finalize below does. Relative error ~1e-5 (max-rel 3e-6 at 4096^3 against a float64
+//     product) at bf16 MFMA rate: 4096^3 + bias in ~0.47 ms against ~1.17 ms on the fp32
+//     MFMA. Roofline: the bf16 peak / 3 (three products per fp32 product).
 //   fp32 MFMA tiles (other 4-element-aligned shapes): v_mfma_f32_32x32x2_f32, exact fp32
 //     products; roofline the fp32 matrix peak (157.3 TFLOP/s).
 //
@@ -526,9 +527,10 @@ hipError_t sgemm_run(bool ta, bool tb, int M, int N, int K, float alpha, const f
     return hk::launch_status();
   }
   // bf16x3 on the BF16 GEMM tiles when every dimension the split copies touch is a multiple
-  // of 8: A and B are split into bf16 hi / lo operands over a tripled k axis, multiplied into
-  // fp32 partials and finished (alpha, beta, bias once) by the split-K finalize. The split-K
-  // of the call is a work-partition hint; this path picks its own.
+  // of 8: A and B are split into bf16 hi / lo operands over a tripled k axis and multiplied on
+  // the BF16 GEMM tiles. With one k split the tiles write C (alpha, beta, bias) themselves;
+  // with more, fp32 partials are finished (alpha, beta, bias once) by the split-K finalize.
+  // The split-K of the call is a work-partition hint; this path picks its own.
   const bool x3_ok = K % 8 == 0 && N % 8 == 0 && (!ta || M % 8 == 0) &&
                      3LL * K < (1 << 22) && (ta ? M : 3LL * K) < (1 << 22) &&
                      (tb ? 3LL * K : N) < (1 << 22) && batchCount <= 65535 &&
@@ -543,7 +545,8 @@ hipError_t sgemm_run(bool ta, bool tb, int M, int N, int K, float alpha, const f
     hk::bgemm_split_plan(M, N, K3, batchCount, &used, &kps);
     auto up = [](int64_t bytes) { return (bytes + 255) & ~int64_t{255}; };
     const int64_t a_bytes = up(na * batchCount * 2), b_bytes = up(nb * batchCount * 2);
-    const int64_t p_bytes = static_cast<int64_t>(used) * batchCount * M * N * 4;
+    // one split: the GEMM tiles write C themselves (alpha, beta, bias), no partials
+    const int64_t p_bytes = used == 1 ? 0 : static_cast<int64_t>(used) * batchCount * M * N * 4;
     void* ws = nullptr;
     HK_RETURN_IF_ERROR(hk::device_workspace(static_cast<size_t>(a_bytes + b_bytes + p_bytes),
                                             stream, &ws));
@@ -569,8 +572,11 @@ hipError_t sgemm_run(bool ta, bool tb, int M, int N, int K, float alpha, const f
                          static_cast<int64_t>(strideB), rows, cols, B3, lb, nb, 0);
       HK_RETURN_IF_ERROR(hk::launch_status());
     }
+    const hk::F32Out out{C,        static_cast<int64_t>(ldc), static_cast<int64_t>(strideC),
+                         ep.alpha, ep.beta, ep.bias, ep.bias_stride, ep.bias_scale};
     HK_RETURN_IF_ERROR(hk::bgemm_partials(ta, tb, M, N, K3, A3, la, na, B3, lb, nb, batchCount,
-                                          used, kps, part, stream));
+                                          used, kps, part, &out, stream));
+    if (used == 1) return hipSuccess;
     return launch_finalize(stream, part, used, batchCount, M, N, C, static_cast<int64_t>(ldc),
                            static_cast<int64_t>(strideC), ep);
   }

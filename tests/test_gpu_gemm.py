@@ -156,7 +156,8 @@ def test_bgemm_baseline_shape_sampled_rows(hk, orc, ta, tb):
 
 
 # ---------------------------------------------------------------------------------------------
-# FP32 SGEMM (blas/fp32): C = alpha op(A) op(B) + beta C + bias, bias added once; fp32 MFMA.
+# FP32 SGEMM (blas/fp32): C = alpha op(A) op(B) + beta C + bias, bias added once; bf16x3 products
+# on the BF16 GEMM tiles for 8-aligned shapes, fp32 MFMA tiles for other 4-aligned ones.
 # Tolerance: BASELINE.json's 2e-3 relative (max|err| / max|ref|) against the oracle's fp32
 # k-order reference (sgemm_test.cu:176-185 restated on the CPU).
 # ---------------------------------------------------------------------------------------------
@@ -237,6 +238,34 @@ def test_sgemm_bias_strides_and_batches(hk, orc):
                 else:
                     ref = ref + bias_np[0]
                 assert max_rel(out[b], ref) <= 2e-3, (stride, split_k, b)
+
+
+@pytest.mark.parametrize("lay", ["NN", "TN"])
+def test_sgemm_one_split_writes_c_from_the_tiles(hk, orc, lay):
+    # 4 batches of 2048 x 2048 fill the device with 256 output tiles, so the bf16x3 path runs
+    # with one k split and the GEMM tiles apply alpha, beta and the bias to C themselves
+    M, N, K, batch = 2048, 2048, 256, 4
+    enum, ta, tb = SG_LAYOUT[lay]
+    say("sgemm one split", lay)
+    As = [_sg_operands(orc, M, N, K, ta, tb, 300 + 10 * b) for b in range(batch)]
+    A = torch.from_numpy(np.stack([x[0] for x in As])).to(DEV)
+    B = torch.from_numpy(np.stack([x[1] for x in As])).to(DEV)
+    C0 = np.stack([x[2] for x in As])
+    full_bias = orc.splitmix_uniform(M * N, 377).reshape(M, N)
+    for stride, bias_np in ((N, As[0][3]), (M * N, full_bias.reshape(-1)), (1, full_bias[0, :1])):
+        C = torch.from_numpy(C0.copy()).to(DEV)
+        out = _sg_call(hk, "hk_sgemm", enum, A, B, C, M, N, K, 1.5, -0.5,
+                       bias=torch.from_numpy(np.ascontiguousarray(bias_np)).to(DEV),
+                       bias_stride=stride, batch=batch, sA=M * K, sB=K * N, sC=M * N)
+        for b in range(batch):
+            ref = orc.sgemm(ta, tb, As[b][0], As[b][1], alpha=1.5, beta=-0.5, C0=C0[b])
+            if stride == N:
+                ref = ref + bias_np
+            elif stride == M * N:  # the reference's (batch % M) * N row (core_template:310)
+                ref = ref + full_bias[b % M]
+            else:
+                ref = ref + bias_np[0]
+            assert max_rel(out[b], ref) <= 2e-3, (stride, b)
 
 
 def test_sgemm_addmm_beta_scaled_bias(hk, orc):
