@@ -75,10 +75,10 @@ class Flusher:
     a 25 MB LayerNorm)."""
 
     def __init__(self):
-        self.buf = torch.ones(512 << 18, dtype=torch.int32, device=DEV)
+        self.buf = torch.ones(512 << 18, dtype=torch.float32, device=DEV)
 
     def __call__(self):
-        self.buf.sum()
+        self.buf.sum()  # one reduction kernel over the fp32 buffer: reads only
 
 
 def time_kernel(fn, reps, flush=None):
