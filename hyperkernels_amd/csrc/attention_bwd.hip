@@ -397,17 +397,23 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
                  rdtr(sKl + rb, tka, tkb), dq);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // dq layout: query 32 qb + 8 (i/4) + 4 hh + i%4, d 32 dbq + c. Key half 1 parks its
-    // partial in the exchange area (read by key half 0 of the previous tile before the
-    // barrier at the top of this one); key half 0 adds it and issues the atomics.
+    // dq layout: query 32 qb + 8 (i/4) + 4 hh + i%4, d 32 dbq + c. The two key halves of a
+    // block split its rows: key half h finishes registers i in [8 h, 8 h + 8) (rows 0 .. 15 or
+    // 16 .. 31 of the block) and parks the other 8 in the exchange area for its partner; each
+    // adds the partner's parked values to its own and issues 8 atomics. The area is read before
+    // the barrier at the top of the next query tile, so the next tile's parking cannot race it.
     float HK_LDS* park = (float HK_LDS*)(lds + kOffPark) + (wave & 3) * (32 * 33);
     float HK_LDS* pbase = park + 4 * hh * 33 + c;
-    if (kh == 1) {
+    auto row_of = [](int i) { return 8 * (i >> 2) + (i & 3); };
+    if (kh == 0) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) pbase[(8 * (i >> 2) + (i & 3)) * 33] = dq[i];
+      for (int i = 8; i < 16; ++i) pbase[row_of(i) * 33] = dq[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pbase[row_of(i) * 33] = dq[i];
     }
     __syncthreads();
-    if (kh == 0) {
+    {
       // wave-uniform row base plus a 32-bit per-lane offset (row 4 hh, column c); the
       // per-register row steps (8 (i/4) + i%4) * stride are uniform too
       const int64_t qblk = q0 + 32 * qb;
@@ -416,7 +422,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
       const bool rows_in = qblk + 32 <= T;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int rs = 8 * (i >> 2) + (i & 3);
+        if ((i >> 3) != kh) continue;  // wave-uniform
+        const int rs = row_of(i);
         if (rows_in || qblk + 4 * hh + rs < T)
           unsafeAtomicAdd(dqu + rs * p.dq_strideM + loff, (dq[i] + pbase[rs * 33]) * p.scale);
       }
