@@ -323,6 +323,10 @@ def time_cases(cases, flush, out):
             peak = W.PEAK_TFLOPS[bound]
             out[name] = {"avg_ms": round(t["avg_ms"], 5), "achieved": round(ach, 1),
                          "unit": "TFLOP/s", "peak": peak, "frac": round(ach / peak, 4)}
+            if bound == "bf16x3":
+                # the same fp32-I/O work priced against the fp32 MFMA peak (the other choice the
+                # north star allows): above 1 means faster than any fp32-MFMA kernel can be
+                out[name]["frac_of_fp32_mfma_peak"] = round(ach / W.PEAK_TFLOPS["fp32_matrix"], 4)
         log(name, out[name])
     return out
 
