@@ -26,6 +26,7 @@
 // make 64). Workgroups are ordered key tile major, so under causal masking the longest ones are
 // dispatched first.
 #include <mutex>
+#include <type_traits>
 
 #include "hk_device.h"
 #include "hk_host.h"
@@ -316,26 +317,38 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
                    rd16(krow + 2 * kKPlane, roff[ks]), rd16(krow + 3 * kKPlane, roff[ks]), dp);
         __builtin_amdgcn_sched_barrier(0);
       }
-      // P and dS in place
+      // P and dS in place. Interior blocks (clean, wave-uniform) take a path without the mask
+      // selects; edge blocks zero P where the query or key lies past T or the key follows the
+      // query under causal masking (offsets relative to the block, 32-bit compares).
+      auto p_ds = [&](auto masked) {
+        const int key_lim = static_cast<int>(min<int64_t>(T - kw, 32));  // keys kw + c < T
+        const int q_lim = static_cast<int>(min<int64_t>(T - qw, 32));    // queries qw + r < T
+        const int cdiff = static_cast<int>(kw - qw);  // key - query = cdiff + c - r
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int qloc = 32 * qh + 8 * g + 4 * hh;
-        const f32x4_t lv = *reinterpret_cast<const f32x4_t HK_LDS*>(sL + qloc);
-        const f32x4_t dv4 = *reinterpret_cast<const f32x4_t HK_LDS*>(sD + qloc);
+        for (int g = 0; g < 4; ++g) {
+          const int qloc = 32 * qh + 8 * g + 4 * hh;
+          const f32x4_t lv = *reinterpret_cast<const f32x4_t HK_LDS*>(sL + qloc);
+          const f32x4_t dv4 = *reinterpret_cast<const f32x4_t HK_LDS*>(sD + qloc);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 4 * g + e;
-          // exponent <= ~0 (scores minus the row's log-sum-exp); hardware exp2
-          float pv = __builtin_amdgcn_exp2f(s[i] * sl2 - lv[e]);
-          if (!clean) {
-            const int64_t qq = q0 + qloc + e;
-            const bool valid = qq < T && key < T && (!p.is_causal || key <= qq);
-            pv = valid ? pv : 0.f;
+          for (int e = 0; e < 4; ++e) {
+            const int i = 4 * g + e;
+            // exponent <= ~0 (scores minus the row's log-sum-exp); hardware exp2
+            float pv = __builtin_amdgcn_exp2f(s[i] * sl2 - lv[e]);
+            if constexpr (decltype(masked)::value) {
+              const int r = 8 * g + 4 * hh + e;  // query row within the block
+              const bool valid =
+                  r < q_lim && c < key_lim && (!p.is_causal || cdiff + c - r <= 0);
+              pv = valid ? pv : 0.f;
+            }
+            s[i] = pv;
+            dp[i] = pv * (dp[i] - dv4[e]);
           }
-          s[i] = pv;
-          dp[i] = pv * (dp[i] - dv4[e]);
         }
-      }
+      };
+      if (clean)
+        p_ds(std::false_type{});
+      else
+        p_ds(std::true_type{});
       // P^T / dS^T as A operands (rows = keys): k-step ks covers the lane's elements
       // 8 ks .. 8 ks + 7, i.e. queries 32 qh + 16 ks + 4 hh + {0..3} and + 8 + {0..3}.
 #pragma unroll
