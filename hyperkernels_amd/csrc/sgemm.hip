@@ -18,7 +18,7 @@
 //     tiles of this library (bgemm.hip) sums ah bh + ah bl + al bh in fp32. With one k split
 //     the GEMM tiles apply alpha, beta and the bias and write C; with more, the split-K
 //     finalize below does. Relative error ~1e-5 (max-rel 3e-6 at 4096^3 against a float64
-//     product) at bf16 MFMA rate: 4096^3 + bias in ~0.47 ms against ~1.17 ms on the fp32
+//     product) at bf16 MFMA rate: 4096^3 + bias in ~0.39 ms against ~1.17 ms on the fp32
 //     MFMA. Roofline: the bf16 peak / 3 (three products per fp32 product).
 //   fp32 MFMA tiles (other 4-element-aligned shapes): v_mfma_f32_32x32x2_f32, exact fp32
 //     products; roofline the fp32 matrix peak (157.3 TFLOP/s).
