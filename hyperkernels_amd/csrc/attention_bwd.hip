@@ -104,28 +104,6 @@ __device__ __forceinline__ f32x16_t mfma3(bf16x8_t ah, bf16x8_t al, bf16x8_t bh,
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, c, 0, 0, 0);
 }
 
-// Operand of 8 consecutive head-dim elements (chunk `chunk`) of row `row`: one 16-byte read.
-__device__ __forceinline__ bf16x8_t rd_row(const char HK_LDS* plane, int row, int chunk) {
-  return *reinterpret_cast<const bf16x8_t HK_LDS*>(plane + off128(row, chunk));
-}
-
-// Transposed operand: the contraction runs over rows. Lane l gets column c0 + l % 32 and rows
-// r0 .. r0 + 3 (elements 0-3) and r1 .. r1 + 3 (elements 4-7), where r0 and r1 may depend on
-// l / 32 and are multiples of 4. ds_read_b64_tr_b16: within each 16-lane group, lane j reads
-// 4 bf16 of row rb + j / 4 at columns cb + 4 (j % 4), and lane i of the group receives column
-// cb + i of rows rb .. rb + 3.
-__device__ __forceinline__ bf16x8_t rd_tr(const char HK_LDS* plane, int c0, int r0, int r1,
-                                          int lane) {
-  const int j = lane & 15;
-  const int col = c0 + 16 * ((lane >> 4) & 1) + 4 * (j & 3);
-  const int ra = r0 + (j >> 2), rb = r1 + (j >> 2);
-  const bf16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (bf16x4_t HK_LDS*)(plane + off128(ra, col >> 3) + (col & 7) * 2));
-  const bf16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (bf16x4_t HK_LDS*)(plane + off128(rb, col >> 3) + (col & 7) * 2));
-  return bf16x8_t{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
-
 // Stages rows [r0, r0 + ROWS) x 64 floats of a strided tensor into a hi / lo plane pair:
 // thread t handles row t / TPR, TPR threads per row, 64 / TPR floats (whole 16-byte chunks)
 // each. Rows at or past T are zero. `reg` holds the fp32 values between load and store so that
@@ -203,7 +181,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
   const int c = lane & 31;
   const int hh = lane >> 5;
   const int kg = wave & 3, qh = wave >> 2;
-  const int64_t key = k0 + 32 * kg + c;  // this lane's key column in S / dP
   const float sl2 = p.scale * kLog2e;
 
   // K and V tiles (128 x 64) once
@@ -244,7 +221,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
   int roff[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) roff[ks] = c * kRowBytes + (((2 * ks + hh) ^ sw_c) << 4);
-  // Transposed reads: lane (group bit g1, index j) addresses row rb + j / 4 at column
+  // Transposed reads (ds_read_b64_tr_b16): within each 16-lane group, lane j reads 4 bf16 of
+  // row rb + j / 4 at columns cb + 4 (j % 4), and lane i of the group receives column cb + i of
+  // rows rb .. rb + 3. Lane (group bit g1, index j) addresses row rb + j / 4 at column
   // cb + 16 g1 + 4 (j % 4); x = chunk of that column within a 32-column block.
   const int j15 = lane & 15, jj = j15 >> 2;
   const int colin = 16 * ((lane >> 4) & 1) + 4 * (j15 & 3);

@@ -108,7 +108,7 @@ struct TileOperand {
   }
   // Byte offset of lane `lane`'s 16 bytes of copy instruction ii (0 .. 31) from the tile's
   // global base at k = 0, and the (row, k) of its first element.
-  __device__ static void source(int ii, int lane, int64_t ld, int& row, int& k) {
+  __device__ static void source(int ii, int lane, int& row, int& k) {
     if (KMAJOR) {
       row = ii * 8 + (lane >> 3);
       k = ((lane & 7) ^ ((row >> 1) & 7)) * 8;
@@ -289,11 +289,11 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
 #pragma unroll
   for (int i = 0; i < kLoadsPerWave; ++i) {
     int row, k;
-    OA::source(wave * kLoadsPerWave + i, lane, lda, row, k);
+    OA::source(wave * kLoadsPerWave + i, lane, row, k);
     row = min(row, (A_KMAJOR ? M - 8 + 7 : M - 8) - m0);  // k-major: a row; else an 8-row chunk
     offA[i] = static_cast<int>(OA::byte_offset(row, k, lda));
     kA[i] = k;
-    OB::source(wave * kLoadsPerWave + i, lane, ldb, row, k);
+    OB::source(wave * kLoadsPerWave + i, lane, row, k);
     row = min(row, (B_KMAJOR ? N - 8 + 7 : N - 8) - n0);
     offB[i] = static_cast<int>(OB::byte_offset(row, k, ldb));
     kB[i] = k;

@@ -137,7 +137,7 @@ __global__ __launch_bounds__(kBcastThreads) void gemv_bcast(int R, int K, int kc
   const uint16_t* xb = x + b * sx;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   int k = kbeg + wave;
-  if (VEC && (blockIdx.x + 1) * kColsPerWave <= R) {
+  if (VEC && static_cast<int>(blockIdx.x + 1) * kColsPerWave <= R) {
     // Every lane of the workgroup owns 8 outputs (uniform branch). Whole rounds: kUnroll rows
     // of 16 bytes in flight per lane with no condition between them; the round's kUnroll x
     // values come from one load spread over the first lanes, broadcast with readlane, so no
