@@ -155,6 +155,37 @@ def test_bgemm_baseline_shape_sampled_rows(hk, orc, ta, tb):
     assert rel <= 1e-2
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+def test_bgemm_partial_last_round_deterministic(hk, orc, ta, tb):
+    # 17 x 17 = 289 output tiles (a last round of 33 on 256 CUs), 17 k-tiles, the last partial.
+    # Rows sampled over every tile row; the same call twice must give the same bits, and the
+    # bias form runs at the same shape.
+    M, N, K = 4352, 4352, 1032
+    say("bgemm partial last round", ta, tb)
+    A, B, C0 = _operands(orc, M, N, K, ta, tb, 800)
+    rows = np.unique(np.concatenate([np.arange(0, M, 37), [M - 1]]))
+    Asub = np.ascontiguousarray(A[:, rows] if ta else A[rows, :])
+    ref = orc.bgemm(ta, tb, Asub, B, alpha=1.0, beta=0.5, C0=np.ascontiguousarray(C0[rows]))
+    first = _run(hk, "hk_bgemm", A, B, C0, M, N, K, ta, tb, 1.0, 0.5)
+    second = _run(hk, "hk_bgemm", A, B, C0, M, N, K, ta, tb, 1.0, 0.5)
+    assert np.array_equal(first, second)
+    rel = max_rel(orc.bf16_to_f32(first[rows]), ref)
+    print(f"rel {rel:.2e}")
+    assert rel <= 1e-2
+    if (ta, tb) == (0, 0):
+        lib = hk.lib()
+        bias = orc.f32_to_bf16(orc.splitmix_uniform(N, 801, -1.0, 1.0))
+        dA, dB, dbias = to_dev_bf16(A), to_dev_bf16(B), to_dev_bf16(bias)
+        dC = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+        stream = torch.cuda.current_stream().cuda_stream
+        assert lib.hk_bgemm_addmm(M, N, K, bits(1.0), dA.data_ptr(), K, 0, dB.data_ptr(), N, 0,
+                                  bits(0.5), dbias.data_ptr(), N, dC.data_ptr(), N, 0, 1,
+                                  stream) == 0
+        out = to_host_bits(dC)
+        refb = orc.bgemm(0, 0, Asub, B, alpha=1.0, beta=0.5, bias=bias)  # bias per column
+        assert max_rel(orc.bf16_to_f32(out[rows]), refb) <= 1e-2
+
+
 # ---------------------------------------------------------------------------------------------
 # FP32 SGEMM (blas/fp32): C = alpha op(A) op(B) + beta C + bias, bias added once; bf16x3 products
 # on the BF16 GEMM tiles for 8-aligned shapes, fp32 MFMA tiles for other 4-aligned ones.
