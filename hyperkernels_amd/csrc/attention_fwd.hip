@@ -261,9 +261,7 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
   // keeps the compiler from sinking each read next to its use, which would expose the full LDS
   // latency before every MFMA).
   auto qk = [&](const char* st, float c0) {
-    f32x16_t sc;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) sc[i] = c0;
+    f32x16_t sc = c0 + f32x16_t{};  // splat
     bf16x8_t kh[4], kl[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
