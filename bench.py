@@ -454,11 +454,15 @@ def gemm_cases(g):
     sbias = torch.randn(S["N"], generator=g, device=DEV) * 0.02
     sc = torch.empty(S["M"], S["N"], device=DEV)
 
-    def run_sgemm():
+    def run_sgemm(split_k):
         assert lib.hk_sgemm(2, S["M"], S["N"], S["K"], 1.0, sa.data_ptr(), S["K"], 0,
                             sb.data_ptr(), S["N"], 0, 0.0, sc.data_ptr(), S["N"], 0,
-                            sbias.data_ptr(), S["N"], 1, S["split_k"], stream()) == 0
-    cases.append(("sgemm_NN_4096^3_splitk4_bias", run_sgemm,
+                            sbias.data_ptr(), S["N"], 1, split_k, stream()) == 0
+    # the config as stated (4 k splits summed by the finalize), and the library's own plan
+    assert lib.hk_sgemm_split_count(2, S["M"], S["N"], S["K"], 1, S["split_k"]) == S["split_k"]
+    cases.append(("sgemm_NN_4096^3_splitk4_bias", lambda: run_sgemm(S["split_k"]),
+                  W.gemm_flop(S["M"], S["N"], S["K"]), "bf16x3"))
+    cases.append(("sgemm_NN_4096^3_auto_split_bias", lambda: run_sgemm(0),
                   W.gemm_flop(S["M"], S["N"], S["K"]), "bf16x3"))
     # the vendor library on the same shapes, for comparison (not part of the surface):
     # torch.matmul -> hipBLASLt; bf16 NN / NT / TN and the fp32 GEMM + bias (fp32 MFMA)

@@ -70,8 +70,8 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 // kernel waits for the copies itself (vmcnt) before the barrier that publishes a stage.
 // Address = sbase (wave-uniform 64-bit, SGPRs) + voff (per-lane byte offset).
 __device__ __forceinline__ void copy16_to_lds(const void* sbase, int voff, unsigned lds_addr) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
-               "s"(lds_addr));
+  // m0 (the LDS destination) is an input operand, so the compiler knows the asm sets it
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr));
 }
 
 // One operand of a k-tile in LDS: 256 rows of M (or N) by BK = 64 k, bf16, 32 KiB.
@@ -599,6 +599,24 @@ int auto_split_k(int64_t work_tiles, int64_t ktiles, int64_t outputs) {
   return best_s;
 }
 
+// Whether a product takes the 256 x 256 MFMA tiles (else the fp32-accumulating bgemm_simple):
+// 8-element multiples for every contiguous extent, leading dimension and batch stride, 16-byte
+// aligned bases, and leading dimensions whose per-lane 32-bit byte offsets fit.
+bool tiled_path(bool ta, bool tb, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
+                int64_t sA, int64_t sB, int64_t sC, bool aligned) {
+  const int contig_a = ta ? M : K, contig_b = tb ? K : N;
+  return (contig_a % 8 == 0) && (contig_b % 8 == 0) && (N % 8 == 0) && (lda % 8 == 0) &&
+         (ldb % 8 == 0) && (ldc % 8 == 0) && (sA % 8 == 0) && (sB % 8 == 0) &&
+         (sC % 8 == 0) && aligned && K > 0 && lda < (1 << 22) && ldb < (1 << 22);
+}
+
+// Number of k splits the tiled path runs for a product (split_k == 0: the library's choice).
+int tiled_splits(int M, int N, int K, int batch, int split_k) {
+  int used = 1, kps = 0;
+  hk::bgemm_split_plan(M, N, K, batch, split_k, &used, &kps);
+  return used;
+}
+
 // bias == NULL: C = alpha * op(A) op(B) + beta * C. Otherwise C = alpha * op(A) op(B) +
 // beta * bias with bias_numel N (per column), M (per row), 1 (scalar) or M*N (full, shared by
 // all batches), tested in that order; C is then only written.
@@ -633,13 +651,8 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
     else return hipErrorInvalidValue;
   }
 
-  const int contig_a = ta ? M : K, contig_b = tb ? K : N;
-  const bool tiled_ok = (contig_a % 8 == 0) && (contig_b % 8 == 0) && (N % 8 == 0) &&
-                        (lda % 8 == 0) && (ldb % 8 == 0) && (ldc % 8 == 0) &&
-                        (strideA % 8 == 0) && (strideB % 8 == 0) && (strideC % 8 == 0) &&
-                        hk::aligned16(A) && hk::aligned16(B) && hk::aligned16(C) && K > 0 &&
-                        // per-lane source offsets inside a tile are 32-bit byte offsets
-                        lda < (1 << 22) && ldb < (1 << 22);
+  const bool tiled_ok = tiled_path(ta, tb, M, N, K, lda, ldb, ldc, strideA, strideB, strideC,
+                                   hk::aligned16(A) && hk::aligned16(B) && hk::aligned16(C));
   if (!tiled_ok) {
     if (K == 0) splitK = 1;
     dim3 grid((N + 15) / 16, (M + 15) / 16, batchCount);
@@ -650,17 +663,15 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
     return hk::launch_status();
   }
   const int64_t tiles = static_cast<int64_t>((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  if (splitK == 0) splitK = auto_split_k(tiles * batchCount, hk::ceil_div(K, BK),
-                                         static_cast<int64_t>(M) * N * batchCount);
-  HK_CHECK_ARG(tiles <= INT32_MAX && static_cast<int64_t>(batchCount) * splitK <= 65535);
-  if (splitK == 1) {
+  // k range per split rounded to the k-tile; `used` splits are not empty
+  int used = 1, kps = K;
+  hk::bgemm_split_plan(M, N, K, batchCount, splitK, &used, &kps);
+  HK_CHECK_ARG(tiles <= INT32_MAX && static_cast<int64_t>(batchCount) * used <= 65535);
+  if (used == 1) {
     dim3 grid(static_cast<unsigned>(tiles), 1, batchCount);
     return dispatch_layout<false>(ta, tb, grid, stream, M, N, K, ep, A, lda, strideA, B, ldb,
                                   strideB, C, ldc, strideC, 1, K, nullptr);
   }
-  // k range per split rounded to the k-tile
-  const int kps = static_cast<int>(hk::ceil_div(hk::ceil_div(K, splitK), BK) * BK);
-  const int used = static_cast<int>(hk::ceil_div(K, kps));
   void* ws = nullptr;
   const size_t part_bytes = static_cast<size_t>(used) * batchCount * M * N * sizeof(float);
   HK_RETURN_IF_ERROR(hk::device_workspace(part_bytes, stream, &ws));
@@ -685,9 +696,11 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
 
 namespace hk {
 
-void bgemm_split_plan(int M, int N, int K, int batch, int* used, int* kps) {
+void bgemm_split_plan(int M, int N, int K, int batch, int split_k, int* used, int* kps) {
   const int64_t tiles = static_cast<int64_t>((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  const int s = auto_split_k(tiles * batch, hk::ceil_div(K, BK), static_cast<int64_t>(M) * N * batch);
+  const int s = split_k > 0 ? split_k
+                            : auto_split_k(tiles * batch, hk::ceil_div(K, BK),
+                                           static_cast<int64_t>(M) * N * batch);
   *kps = static_cast<int>(hk::ceil_div(hk::ceil_div(K, s), BK) * BK);
   *used = static_cast<int>(hk::ceil_div(K, *kps));
 }
@@ -711,6 +724,21 @@ hipError_t bgemm_partials(bool ta, bool tb, int M, int N, int K, const hk_bf16* 
 }
 
 }  // namespace hk
+
+extern "C" int hk_bgemm_split_count(int transA, int transB, int M, int N, int K, int batchCount,
+                                    int splitK) {
+  if (transA < 0 || transA > 2 || transB < 0 || transB > 2 || M < 0 || N < 0 || K < 0 ||
+      batchCount < 0 || splitK < 0)
+    return -1;
+  if (M == 0 || N == 0 || batchCount == 0) return 0;
+  const bool ta = transA != 0, tb = transB != 0;
+  if (splitK == 0 && (M == 1 || N == 1)) return 1;  // the GEMV kernels
+  const int64_t lda = ta ? M : K, ldb = tb ? K : N;
+  if (!tiled_path(ta, tb, M, N, K, lda, ldb, N, lda * (ta ? K : M), ldb * (tb ? N : K),
+                  static_cast<int64_t>(M) * N, true))
+    return 1;
+  return tiled_splits(M, N, K, batchCount, splitK);
+}
 
 extern "C" hipError_t hk_bgemm(int transA, int transB, int M, int N, int K, hk_bf16 alpha,
                                const hk_bf16* A, int lda, long long strideA, const hk_bf16* B,

@@ -57,8 +57,9 @@ struct F32Out {
 // part[s][batch][M][N] (s < used) of op(A) op(B) over k-range [s kps, (s + 1) kps); their sum
 // in split order is the product. With used == 1 and out != NULL the tiles write out->C through
 // its epilogue instead (part is not touched). Needs the tiled path's alignment: 8-element
-// multiples and 16-byte aligned bases. bgemm_split_plan picks (used, kps) for a shape.
-void bgemm_split_plan(int M, int N, int K, int batch, int* used, int* kps);
+// multiples and 16-byte aligned bases. bgemm_split_plan picks (used, kps) for a shape: split_k
+// ranges of kps k each (split_k == 0: the library's choice), `used` of them non-empty.
+void bgemm_split_plan(int M, int N, int K, int batch, int split_k, int* used, int* kps);
 hipError_t bgemm_partials(bool ta, bool tb, int M, int N, int K, const hk_bf16* A, int64_t lda,
                           int64_t sA, const hk_bf16* B, int64_t ldb, int64_t sB, int batch,
                           int used, int kps, float* part, const F32Out* out,

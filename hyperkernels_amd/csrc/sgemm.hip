@@ -59,8 +59,8 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 // wait for all outstanding copies (the kernel orders them itself with vmcnt + barrier).
 // Address = sbase (wave-uniform 64-bit) + voff (per-lane byte offset).
 __device__ __forceinline__ void copy16_to_lds(const void* sbase, int voff, unsigned lds_addr) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
-               "s"(lds_addr));
+  // m0 (the LDS destination) is an input operand, so the compiler knows the asm sets it
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr));
 }
 
 // One operand of a k-tile in LDS: 256 rows of M (or N) by BK = 32 k, fp32, 32 KiB.
@@ -423,12 +423,17 @@ __global__ __launch_bounds__(256) void sgemm_simple(int ta, int tb, int M, int N
 
 // bf16x3 operand of an fp32 matrix X (rows x cols, leading dimension ldx, batch stride sx):
 // each x = hi + lo (bf16, round to nearest even, |x - hi - lo| <= 2^-18 |x|) and the k axis is
-// tripled into three segments, (hi, hi, lo) for the left operand and (hi, lo, hi) for the right,
-// so that a bf16 GEMM over 3K sums ah bh + ah bl + al bh. KCOLS: k runs along the columns
-// (Y[r][s cols + c]); otherwise along the rows (Y[s rows + r][c]). Four columns per thread
-// (cols % 4 == 0, 16-byte aligned rows): one 16-byte load, three 8-byte stores; batch b in
-// blockIdx.y and a 32-bit index within one matrix (rows * cols / 4 < 2^31, checked by the
+// tripled into three segments, (hi, hi', lo) for the left operand and (hi, lo, hi') for the
+// right, so that a bf16 GEMM over 3K sums ah bh + ah' bl + al bh'. KCOLS: k runs along the
+// columns (Y[r][s cols + c]); otherwise along the rows (Y[s rows + r][c]). Four columns per
+// thread (cols % 4 == 0, 16-byte aligned rows): one 16-byte load, three 8-byte stores; batch b
+// in blockIdx.y and a 32-bit index within one matrix (rows * cols / 4 < 2^31, checked by the
 // host). Runs at copy rate (a measured ~6.8 TB/s for 4096 x 4096).
+// Non-finite x (inf, NaN, or a finite value that rounds past bf16's largest one): hi carries
+// it, lo and hi' (the copy of hi in the cross term) are 0. The cross terms of its products are
+// then 0 and the product is hi * bh alone, +-inf or NaN as the reference's TF32 product is;
+// with lo = bf16(x - hi) and hi' = hi they would add inf * bl (NaN for bl = 0 or of the other
+// sign) and bf16(inf - inf) = NaN.
 template <bool KCOLS>
 __global__ __launch_bounds__(256) void split3(const float* __restrict__ X, int64_t ldx, int64_t sx,
                                               int rows, int cols, uint16_t* __restrict__ Y,
@@ -440,18 +445,21 @@ __global__ __launch_bounds__(256) void split3(const float* __restrict__ X, int64
   const unsigned r = i / c4, c = (i - r * c4) * 4;
   const f32x4_t v =
       *reinterpret_cast<const f32x4_t*>(X + b * sx + static_cast<int64_t>(r) * ldx + c);
-  uint32_t hv[2], lv[2];
+  uint16_t h[4], l[4], hc[4];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const uint16_t h0 = hk::f32_to_bf16(v[2 * k]), h1 = hk::f32_to_bf16(v[2 * k + 1]);
-    const uint16_t l0 = hk::f32_to_bf16(v[2 * k] - hk::bf16_to_f32(h0));
-    const uint16_t l1 = hk::f32_to_bf16(v[2 * k + 1] - hk::bf16_to_f32(h1));
-    hv[k] = h0 | (static_cast<uint32_t>(h1) << 16);
-    lv[k] = l0 | (static_cast<uint32_t>(l1) << 16);
+  for (int k = 0; k < 4; ++k) {
+    h[k] = hk::f32_to_bf16(v[k]);
+    const bool finite = (h[k] & 0x7f80u) != 0x7f80u;
+    l[k] = finite ? hk::f32_to_bf16(v[k] - hk::bf16_to_f32(h[k])) : uint16_t{0};
+    hc[k] = finite ? h[k] : uint16_t{0};
   }
-  const uint2 H = make_uint2(hv[0], hv[1]), L = make_uint2(lv[0], lv[1]);
+  auto pack = [](const uint16_t (&e)[4]) {
+    return make_uint2(e[0] | (static_cast<uint32_t>(e[1]) << 16),
+                      e[2] | (static_cast<uint32_t>(e[3]) << 16));
+  };
+  const uint2 H = pack(h), L = pack(l), Hc = pack(hc);
   uint16_t* Yb = Y + b * sy;
-  const uint2 seg[3] = {H, left ? H : L, left ? L : H};
+  const uint2 seg[3] = {H, left ? Hc : L, left ? L : Hc};
 #pragma unroll
   for (int sg = 0; sg < 3; ++sg) {
     uint16_t* dst = KCOLS ? Yb + static_cast<int64_t>(r) * ldy + sg * cols + c
@@ -496,12 +504,54 @@ hipError_t dispatch_layout(bool ta, bool tb, dim3 grid, hipStream_t stream, int 
                                       ep, split_k, kps, part);
 }
 
+// The three product paths of an fp32 GEMM and the k-split plan each runs.
+enum class SgemmPath { kSimple, kBf16x3, kFp32Tiles };
+
+// Which path takes a product. Tiles: 4-element multiples for every contiguous extent, leading
+// dimension and batch stride, 16-byte aligned bases. bf16x3 additionally needs every dimension
+// the split copies touch to be a multiple of 8 and the tripled k axis to fit the BF16 tiles'
+// 32-bit per-lane offsets.
+SgemmPath sgemm_path(bool ta, bool tb, int M, int N, int K, int64_t lda, int64_t ldb,
+                     int64_t ldc, int64_t sA, int64_t sB, int64_t sC, int batchCount,
+                     bool aligned) {
+  const int contig_a = ta ? M : K, contig_b = tb ? K : N;
+  const bool tiled_ok = (contig_a % 4 == 0) && (contig_b % 4 == 0) && (N % 4 == 0) &&
+                        (lda % 4 == 0) && (ldb % 4 == 0) && (ldc % 4 == 0) && (sA % 4 == 0) &&
+                        (sB % 4 == 0) && (sC % 4 == 0) && aligned && K > 0 &&
+                        // per-lane source offsets inside a tile are 32-bit byte offsets
+                        lda < (1 << 21) && ldb < (1 << 21);
+  if (!tiled_ok) return SgemmPath::kSimple;
+  const bool x3_ok = K % 8 == 0 && N % 8 == 0 && (!ta || M % 8 == 0) &&
+                     3LL * K < (1 << 22) && (ta ? M : 3LL * K) < (1 << 22) &&
+                     (tb ? 3LL * K : N) < (1 << 22) && batchCount <= 65535 &&
+                     static_cast<int64_t>(M) * K < (int64_t{1} << 33) &&
+                     static_cast<int64_t>(K) * N < (int64_t{1} << 33);
+  return x3_ok ? SgemmPath::kBf16x3 : SgemmPath::kFp32Tiles;
+}
+
+// k-split plan of the fp32 MFMA tiles (BK = 32 fp32 per k-tile): split_k ranges of kps k, the
+// `used` non-empty ones run (split_k == 0: the library's choice, the BF16 tiles' cost model on
+// this path's k-tiles).
+void fp32_split_plan(int M, int N, int K, int batch, int split_k, int* used, int* kps) {
+  int s = split_k;
+  if (s == 0) {
+    int u = 1, kp = 0;
+    // the BF16 planner counts 64-deep k-tiles: 2 K of them are this path's 32-deep ones
+    hk::bgemm_split_plan(M, N, 2 * K, batch, 0, &u, &kp);
+    s = u;
+  }
+  *kps = static_cast<int>(hk::ceil_div(hk::ceil_div(K, s), BK) * BK);
+  *used = static_cast<int>(hk::ceil_div(K, *kps));
+}
+
 hipError_t sgemm_run(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, int lda,
                      long long strideA, const float* B, int ldb, long long strideB, float beta,
                      float* C, int ldc, long long strideC, const float* bias,
                      long long bias_stride, float bias_scale, int batchCount, int splitK,
                      hipStream_t stream) {
-  HK_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batchCount >= 0 && splitK >= 1);
+  // splitK == 0: the library picks the split; otherwise K is cut into splitK ranges (rounded
+  // to the k-tile) whose fp32 partials are summed in split order
+  HK_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batchCount >= 0 && splitK >= 0);
   if (M == 0 || N == 0 || batchCount == 0) return hipSuccess;
   HK_CHECK_ARG(C != nullptr && ldc >= N);
   HK_CHECK_ARG(K == 0 || (A != nullptr && B != nullptr));
@@ -511,14 +561,10 @@ hipError_t sgemm_run(bool ta, bool tb, int M, int N, int K, float alpha, const f
                  bias_stride == 1);
   }
   const Epilogue ep{alpha, beta, bias, bias ? static_cast<int64_t>(bias_stride) : 0, bias_scale};
-  const int contig_a = ta ? M : K, contig_b = tb ? K : N;
-  const bool tiled_ok = (contig_a % 4 == 0) && (contig_b % 4 == 0) && (N % 4 == 0) &&
-                        (lda % 4 == 0) && (ldb % 4 == 0) && (ldc % 4 == 0) &&
-                        (strideA % 4 == 0) && (strideB % 4 == 0) && (strideC % 4 == 0) &&
-                        hk::aligned16(A) && hk::aligned16(B) && hk::aligned16(C) && K > 0 &&
-                        // per-lane source offsets inside a tile are 32-bit byte offsets
-                        lda < (1 << 21) && ldb < (1 << 21);
-  if (!tiled_ok) {
+  const SgemmPath path = sgemm_path(ta, tb, M, N, K, lda, ldb, ldc, strideA, strideB, strideC,
+                                    batchCount,
+                                    hk::aligned16(A) && hk::aligned16(B) && hk::aligned16(C));
+  if (path == SgemmPath::kSimple) {
     dim3 grid((N + 15) / 16, (M + 15) / 16, batchCount);
     hipLaunchKernelGGL(sgemm_simple, grid, dim3(256), 0, stream, ta ? 1 : 0, tb ? 1 : 0, M, N, K,
                        A, static_cast<int64_t>(lda), static_cast<int64_t>(strideA), B,
@@ -530,19 +576,14 @@ hipError_t sgemm_run(bool ta, bool tb, int M, int N, int K, float alpha, const f
   // of 8: A and B are split into bf16 hi / lo operands over a tripled k axis and multiplied on
   // the BF16 GEMM tiles. With one k split the tiles write C (alpha, beta, bias) themselves;
   // with more, fp32 partials are finished (alpha, beta, bias once) by the split-K finalize.
-  // The split-K of the call is a work-partition hint; this path picks its own.
-  const bool x3_ok = K % 8 == 0 && N % 8 == 0 && (!ta || M % 8 == 0) &&
-                     3LL * K < (1 << 22) && (ta ? M : 3LL * K) < (1 << 22) &&
-                     (tb ? 3LL * K : N) < (1 << 22) && batchCount <= 65535 &&
-                     static_cast<int64_t>(M) * K < (int64_t{1} << 33) &&
-                     static_cast<int64_t>(K) * N < (int64_t{1} << 33);
-  if (x3_ok) {
+  // The call's splitK cuts the tripled k axis into that many ranges (0: the library's choice).
+  if (path == SgemmPath::kBf16x3) {
     const int K3 = 3 * K;
     // A' is [M][3K] (k-major) or [3K][M]; B' is [3K][N] or [N][3K]
     const int64_t la = ta ? M : K3, lb = tb ? K3 : N;
     const int64_t na = static_cast<int64_t>(M) * K3, nb = static_cast<int64_t>(K3) * N;
     int used = 1, kps = 0;
-    hk::bgemm_split_plan(M, N, K3, batchCount, &used, &kps);
+    hk::bgemm_split_plan(M, N, K3, batchCount, splitK, &used, &kps);
     auto up = [](int64_t bytes) { return (bytes + 255) & ~int64_t{255}; };
     const int64_t a_bytes = up(na * batchCount * 2), b_bytes = up(nb * batchCount * 2);
     // one split: the GEMM tiles write C themselves (alpha, beta, bias), no partials
@@ -581,14 +622,14 @@ hipError_t sgemm_run(bool ta, bool tb, int M, int N, int K, float alpha, const f
                            static_cast<int64_t>(strideC), ep);
   }
   const int64_t tiles = static_cast<int64_t>((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  HK_CHECK_ARG(tiles <= INT32_MAX && static_cast<int64_t>(batchCount) * splitK <= 65535);
-  if (splitK == 1) {
+  int used = 1, kps = K;
+  fp32_split_plan(M, N, K, batchCount, splitK, &used, &kps);
+  HK_CHECK_ARG(tiles <= INT32_MAX && static_cast<int64_t>(batchCount) * used <= 65535);
+  if (used == 1) {
     dim3 grid(static_cast<unsigned>(tiles), 1, batchCount);
     return dispatch_layout<false>(ta, tb, grid, stream, M, N, K, A, lda, strideA, B, ldb, strideB,
                                   C, ldc, strideC, ep, 1, K, nullptr);
   }
-  const int kps = static_cast<int>(hk::ceil_div(hk::ceil_div(K, splitK), BK) * BK);
-  const int used = static_cast<int>(hk::ceil_div(K, kps));
   void* ws = nullptr;
   HK_RETURN_IF_ERROR(hk::device_workspace(
       static_cast<size_t>(used) * batchCount * M * N * sizeof(float), stream, &ws));
@@ -609,6 +650,23 @@ bool layout_trans(int layout, bool* ta, bool* tb) {
 
 }  // namespace
 
+extern "C" int hk_sgemm_split_count(int layout, int M, int N, int K, int batchCount, int splitK) {
+  bool ta, tb;
+  if (!layout_trans(layout, &ta, &tb) || M < 0 || N < 0 || K < 0 || batchCount < 0 || splitK < 0)
+    return -1;
+  if (M == 0 || N == 0 || batchCount == 0) return 0;
+  const int64_t lda = ta ? M : K, ldb = tb ? K : N;
+  const SgemmPath path = sgemm_path(ta, tb, M, N, K, lda, ldb, N, lda * (ta ? K : M),
+                                    ldb * (tb ? N : K), static_cast<int64_t>(M) * N, batchCount,
+                                    true);
+  int used = 1, kps = 0;
+  if (path == SgemmPath::kBf16x3)
+    hk::bgemm_split_plan(M, N, 3 * K, batchCount, splitK, &used, &kps);
+  else if (path == SgemmPath::kFp32Tiles)
+    fp32_split_plan(M, N, K, batchCount, splitK, &used, &kps);
+  return used;
+}
+
 extern "C" hipError_t hk_sgemm(int layout, int M, int N, int K, float alpha, const float* A,
                                int lda, long long strideA, const float* B, int ldb,
                                long long strideB, float beta, float* C, int ldc,
@@ -626,7 +684,7 @@ extern "C" hipError_t hk_sgemm_addmm(int M, int N, int K, float alpha, const flo
                                      int64_t bias_numel, float* C, int ldc, long long strideC,
                                      int batchCount, hipStream_t stream) {
   return sgemm_run(false, false, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, C, ldc,
-                   strideC, bias, bias_numel, beta, batchCount, 1, stream);
+                   strideC, bias, bias_numel, beta, batchCount, 0, stream);
 }
 
 extern "C" hipError_t hk_sgemm_layout(int layout, int M, int N, int K, float alpha,

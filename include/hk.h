@@ -274,6 +274,11 @@ HK_API hipError_t hk_reduce_generic_f32(const float* src, float* dst, int out_nd
  * hk_bgemm and the two backward entry points have no split argument (as in the reference); the
  *   library splits K itself when the output has too few 256 x 256 tiles to fill the device
  *   (same fp32 partials and split-order sum as hk_bgemm_core).
+ * hk_bgemm_split_count (no counterpart in the reference: a host-only planning query for callers
+ *   and tests that check which plan runs) returns the number of k splits a product of this
+ *   shape runs with (contiguous operands, 16-byte aligned): splitK = 0 for hk_bgemm and the
+ *   backward entry points (the library's choice), the hk_bgemm_core argument otherwise. 1 for
+ *   the GEMV and fallback kernels, 0 for an empty product, -1 for an invalid argument.
  * Any M, N, K; the MFMA path needs the contiguous extents, leading dimensions and strides to
  * be multiples of 8 and 16-byte aligned pointers (the reference's own precondition,
  * bgemm_test.cu:252-256); other shapes run on a slower fp32-accumulating kernel.
@@ -297,6 +302,8 @@ HK_API hipError_t hk_bgemm_tn_backward(int M, int N, int K, hk_bf16 alpha, const
                                        int lda, long long strideA, const hk_bf16* B, int ldb,
                                        long long strideB, hk_bf16 beta, hk_bf16* C, int ldc,
                                        long long strideC, int batchCount, hipStream_t stream);
+HK_API int hk_bgemm_split_count(int transA, int transB, int M, int N, int K, int batchCount,
+                                int splitK);
 
 /* ------------------------------------------------------------------------------------------
  * Batched BF16 GEMV, the M == 1 / N == 1 GEMMs, fp32 accumulation, one bf16 rounding.
@@ -361,16 +368,23 @@ HK_API hipError_t hk_bgemm_core_bias(int layout, int splitK, int M, int N, int K
  *   (the reference's split-K path adds it once per split). bias may be NULL; otherwise
  *   bias_stride selects it as in the reference (:303-315): N -> bias[col];
  *   M*N -> bias[(batch % M) * N + col]; 1 -> bias[0]; any other value is rejected.
- *   splitK >= 1 (the reference's split-K pre-scale kernel sgemm_sm89_scale_kernel, :329-333, is
- *   folded in: no caller pre-pass is needed).
+ *   splitK >= 1 cuts the k loop into splitK ranges as the reference does (k_chunk rounded to
+ *   the k-tile, :123-126; on the bf16x3 path the tripled k axis) whose fp32 partials are summed
+ *   in split order; splitK = 0 lets the library choose. The reference's split-K pre-scale
+ *   kernel sgemm_sm89_scale_kernel (:329-333) is folded in: no caller pre-pass is needed.
  * hk_sgemm_addmm replaces sgemm_addmm_sm89_kernel (blas/fp32/sgemm_addmm_sm89_kernel.cu:66-76):
  *   NN, C = alpha * A B + beta * C + beta * bias, bias_numel in {1, N, M*N} as there.
  * hk_sgemm_layout replaces every tile-specialised SGEMM kernel (sgemm_nn_256x128_sm89_2_opt_k,
  *   sgemm_nn_256x64_sm89_2_k, sgemm_nn_64x64_sm89_2_k, sgemm_nn_256x128_bypass_sm89_batched_kernel,
  *   sgemm_nt_{256x128,128x128,64x128}_sm89_2_k, sgemm_tn_256x128_sm89_optimized,
  *   sgemm_tn_{128x128,256x64}_sm89_2_k, sgemm_tn_{64x64,32x32}_sm89_k): the same product
- *   C = alpha * op(A) op(B) + beta * C for the kernel's layout (pass splitK = 1 for kernels
- *   without a splitK argument). The tile shape is the library's choice.
+ *   C = alpha * op(A) op(B) + beta * C for the kernel's layout (splitK as for hk_sgemm; pass 1
+ *   for kernels without a splitK argument, or 0 to let the library split). The tile shape is
+ *   the library's choice.
+ * hk_sgemm_split_count (no counterpart in the reference: a host-only planning query) returns
+ *   the number of k splits hk_sgemm / hk_sgemm_layout run for this shape and splitK
+ *   (contiguous operands, 16-byte aligned): 1 on the k-order fallback, 0 for an empty product,
+ *   -1 for an invalid argument. hk_sgemm_addmm runs with splitK = 0.
  * Any M, N, K; the MFMA path needs the contiguous extents, leading dimensions and strides to
  * be multiples of 4 and 16-byte aligned pointers (sgemm_test.cu:240-243); other shapes run on a
  * slower k-order kernel.
@@ -388,6 +402,7 @@ HK_API hipError_t hk_sgemm_layout(int layout, int M, int N, int K, float alpha, 
                                   long long strideB, float beta, float* C, int ldc,
                                   long long strideC, int batchCount, int splitK,
                                   hipStream_t stream);
+HK_API int hk_sgemm_split_count(int layout, int M, int N, int K, int batchCount, int splitK);
 
 /* ------------------------------------------------------------------------------------------
  * Attention, fp32 I/O, head_dim 64 (the reference's only instantiation), products as a bf16x3

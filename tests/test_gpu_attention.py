@@ -68,19 +68,24 @@ def test_attn_forward_strided_bthd_layout(hk, orc):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-def test_attn_forward_baseline_shape_sampled_heads(hk, orc, causal):
-    # B=8, H=12, T=1024, d=64, Q, K, V ~ N(0, 1). The GPU computes all 96
-    # heads; the oracle checks 4 of them in full.
+def test_attn_forward_baseline_shape_all_heads(hk, orc, causal):
+    # B=8, H=12, T=1024, d=64, Q, K, V ~ N(0, 1). Every one of the 96
+    # (batch, head) pairs is checked in full against the oracle, and each head on its own (a
+    # head-wise bound, so one wrong head cannot hide under the others' magnitude).
     B, H, T, D = 8, 12, 1024, 64
-    say("attn fwd baseline", causal)
+    say("attn fwd baseline all heads", causal)
     q, k, v = _qkv(orc, B, H, T, D, (31, 32, 33), normal=True)
     o, lse = hk.fused_attn_forward(*(torch.from_numpy(a).to(DEV) for a in (q, k, v)), causal)
     torch.cuda.synchronize()
     o, lse = o.cpu().numpy(), lse.cpu().numpy()
-    for (b, h) in ((0, 0), (3, 7), (5, 2), (7, 11)):
-        sl = (slice(b, b + 1), slice(h, h + 1))
-        ro, rl = orc.attn_forward(q[sl], k[sl], v[sl], 0.125, causal)
-        assert max_rel(o[sl], ro) <= 2e-3 and max_rel(lse[sl], rl) <= 2e-3, (b, h)
+    ro, rl = orc.attn_forward(q, k, v, 0.125, causal)
+    worst = max((max_rel(o[b, h], ro[b, h]), max_rel(lse[b, h], rl[b, h]), (b, h))
+                for b in range(B) for h in range(H))
+    print(f"worst head {worst[2]}: O rel {worst[0]:.2e} LSE rel {worst[1]:.2e}")
+    for b in range(B):
+        for h in range(H):
+            assert max_rel(o[b, h], ro[b, h]) <= 2e-3, (b, h)
+            assert max_rel(lse[b, h], rl[b, h]) <= 2e-3, (b, h)
     if causal:  # invariant: row 0 attends to key 0 only -> O[.,.,0] = V[.,.,0]
         np.testing.assert_allclose(o[:, :, 0], v[:, :, 0], rtol=1e-5, atol=1e-6)
 
@@ -150,11 +155,12 @@ def test_attn_backward_dq_accumulates(hk, orc):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-def test_attn_backward_baseline_shape_sampled_heads(hk, orc, causal):
-    # B=8, H=12, T=1024, d=64, dO ~ N(0, 1), forward's O / LSE reused.
-    # The GPU runs all 96 heads; the oracle checks 2 heads in full.
+def test_attn_backward_baseline_shape_all_heads(hk, orc, causal):
+    # B=8, H=12, T=1024, d=64, dO ~ N(0, 1), forward's O / LSE reused (the
+    # GPU chain forward -> precompute D -> backward). Every one of the 96 (batch, head) pairs
+    # is checked in full against the oracle, head by head.
     B, H, T, D = 8, 12, 1024, 64
-    say("attn bwd baseline", causal)
+    say("attn bwd baseline all heads", causal)
     q, k, v, do = _qkv(orc, B, H, T, D, (71, 72, 73, 74), normal=True)
     Q, K, V, dO = (torch.from_numpy(a).to(DEV) for a in (q, k, v, do))
     O, L = hk.fused_attn_forward(Q, K, V, causal)
@@ -162,13 +168,15 @@ def test_attn_backward_baseline_shape_sampled_heads(hk, orc, causal):
     dq, dk, dv = hk.attn_backward(Q, K, V, dO, L, Dt, causal)
     torch.cuda.synchronize()
     dq, dk, dv = dq.cpu().numpy(), dk.cpu().numpy(), dv.cpu().numpy()
-    for (b, h) in ((0, 0), (6, 9)):
-        sl = (slice(b, b + 1), slice(h, h + 1))
-        ro, rl = orc.attn_forward(q[sl], k[sl], v[sl], 0.125, causal)
-        _, rdq, rdk, rdv = orc.attn_backward(q[sl], k[sl], v[sl], ro, do[sl], rl, 0.125, causal)
-        rels = [max_rel(g[sl], r) for g, r in ((dq, rdq), (dk, rdk), (dv, rdv))]
-        print(f"head {(b, h)}: dQ {rels[0]:.2e} dK {rels[1]:.2e} dV {rels[2]:.2e}")
-        assert max(rels) <= 2e-3, rels
+    ro, rl = orc.attn_forward(q, k, v, 0.125, causal)
+    _, rdq, rdk, rdv = orc.attn_backward(q, k, v, ro, do, rl, 0.125, causal)
+    worst = [0.0, 0.0, 0.0]
+    for b in range(B):
+        for h in range(H):
+            rels = [max_rel(g[b, h], r[b, h]) for g, r in ((dq, rdq), (dk, rdk), (dv, rdv))]
+            worst = [max(w, x) for w, x in zip(worst, rels)]
+            assert max(rels) <= 2e-3, ((b, h), rels)
+    print(f"worst over 96 heads: dQ {worst[0]:.2e} dK {worst[1]:.2e} dV {worst[2]:.2e}")
 
 
 def test_attn_precompute_D(hk, orc):

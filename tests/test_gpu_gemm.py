@@ -106,6 +106,58 @@ def test_bgemm_backward_entry_points(hk, orc):
            1, 0, 2.0, 1.0)
 
 
+def _tile_rows(M):
+    """About 96 rows spread over M, at least one in every 256-row output tile, plus the last."""
+    rows = np.unique(np.concatenate([np.arange(0, M, max(1, M // 96)), [M - 1]]))
+    assert len(np.unique(rows // 256)) == -(-M // 256)
+    return rows
+
+
+@pytest.mark.parametrize("which", ["dA_NT", "dB_TN"])
+def test_bgemm_backward_baseline_shapes_library_split(hk, orc, which):
+    # BASELINE configs[4] backward of Y[8192, 5120] = X[8192, 1280] W[1280, 5120]:
+    #   dA = dY W^T: hk_bgemm_nt_backward, M=8192, N=1280, K=5120 (bgemm_backward_nt…:23-32);
+    #   dB = X^T dY: hk_bgemm_tn_backward, M=1280, N=5120, K=8192 (bgemm_backward_tn…:25-34).
+    # Both have too few 256 x 256 output tiles to fill the device, so the library splits K
+    # itself (fp32 partials + split-order finalize): the path the bench times. A, B ~
+    # N(0, 1/sqrt(K)); rows in every 256-row tile are checked in full against the oracle, with
+    # alpha / beta both active; two runs must give the same bits.
+    lib = hk.lib()
+    if which == "dA_NT":
+        fn, (M, N, K), (ta, tb) = "hk_bgemm_nt_backward", (8192, 1280, 5120), (0, 1)
+    else:
+        fn, (M, N, K), (ta, tb) = "hk_bgemm_tn_backward", (1280, 5120, 8192), (1, 0)
+    splits = lib.hk_bgemm_split_count(ta, tb, M, N, K, 1, 0)
+    say("bgemm backward baseline", which, "splits", splits)
+    assert splits >= 2
+    A, B, C0 = _operands(orc, M, N, K, ta, tb, 1000 + M, normal=True)
+    first = _run(hk, fn, A, B, C0, M, N, K, ta, tb, 1.0, 0.5)
+    second = _run(hk, fn, A, B, C0, M, N, K, ta, tb, 1.0, 0.5)
+    assert np.array_equal(first, second)
+    rows = _tile_rows(M)
+    Asub = np.ascontiguousarray(A[:, rows] if ta else A[rows, :])
+    ref = orc.bgemm(ta, tb, Asub, B, alpha=1.0, beta=0.5, C0=np.ascontiguousarray(C0[rows]))
+    rel = max_rel(orc.bf16_to_f32(first[rows]), ref)
+    print(f"{which} rel {rel:.2e} over {len(rows)} rows")
+    assert rel <= 1e-2
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_bgemm_long_k_library_split_deterministic(hk, orc, ta, tb):
+    # One output tile and 128 k-tiles: the library's split-K choice is >= 2 splits; the fp32
+    # partials are summed in split order, so two runs are bit-identical and match the oracle.
+    M, N, K = 256, 256, 8192
+    lib = hk.lib()
+    splits = lib.hk_bgemm_split_count(ta, tb, M, N, K, 1, 0)
+    say("bgemm long K", ta, tb, "splits", splits)
+    assert splits >= 2
+    A, B, C0 = _operands(orc, M, N, K, ta, tb, 1100)
+    first = _run(hk, "hk_bgemm", A, B, C0, M, N, K, ta, tb, 1.0, 0.5)
+    second = _run(hk, "hk_bgemm", A, B, C0, M, N, K, ta, tb, 1.0, 0.5)
+    assert np.array_equal(first, second)
+    _check(orc, first, A, B, C0, ta, tb, 1.0, 0.5)
+
+
 @pytest.mark.parametrize("M,N,K,ta,tb", [(17, 9, 33, 0, 0), (33, 65, 7, 1, 1), (64, 64, 8, 1, 0),
                                          (300, 260, 72, 0, 1),
                                          # MFMA path with partial M / N tiles and a K tail
@@ -233,9 +285,16 @@ def _sg_call(hk, fn, layout, A, B, C, M, N, K, alpha, beta, bias=None, bias_stri
 
 @pytest.mark.parametrize("M,N,K", SG_HARNESS)
 @pytest.mark.parametrize("lay", ["NN", "NT", "TN"])
-@pytest.mark.parametrize("split_k", [1, 4])
+@pytest.mark.parametrize("split_k", [0, 1, 4])
 def test_sgemm_harness_sizes_bias_split_k(hk, orc, M, N, K, lay, split_k):
+    # split_k >= 1 cuts the k loop into split_k ranges of whole 64-deep k-tiles (the bf16x3
+    # path's k axis is 3 K long), as the reference's k_chunk rounds to its 16-deep tiles
+    # (sgemm_sm89_core_template.cu:126): the non-empty ranges run. 0 is the library's choice.
     enum, ta, tb = SG_LAYOUT[lay]
+    if split_k:
+        ktiles = -(-3 * K // 64)
+        per = -(-ktiles // split_k)
+        assert hk.lib().hk_sgemm_split_count(enum, M, N, K, 1, split_k) == -(-ktiles // per)
     say("sgemm", lay, M, N, K, split_k)
     A, B, C0, bias = _sg_operands(orc, M, N, K, ta, tb, 7 + M)
     out = _sg_call(hk, "hk_sgemm", enum, torch.from_numpy(A).to(DEV), torch.from_numpy(B).to(DEV),
@@ -349,15 +408,23 @@ def test_sgemm_ragged(hk, orc, M, N, K, lay):
 
 
 @pytest.mark.parametrize("lay", ["NN", "NT", "TN"])
-def test_sgemm_baseline_shape_split_k4_sampled_rows(hk, orc, lay):
-    # 4096^3, split-K 4, fused bias; 64 rows checked against the oracle.
+@pytest.mark.parametrize("split_k", [4, 0])
+def test_sgemm_baseline_shape_split_k4_sampled_rows(hk, orc, lay, split_k):
+    # 4096^3 with split-K 4 (4 k splits really run: fp32 partials summed
+    # in split order by the finalize) and the fused bias; split_k 0 is the library's own plan.
+    # beta = 1 with C0 ~ N(0, 1) and the bias ~ N(0, 0.02) against a product of std 1/64: a
+    # bias added once per split (the reference's split-K epilogue) would be off by 3 * bias,
+    # ~8x the 2e-3 bound, and beta * C applied per split by 3 * C0. 64 rows checked in full.
     enum, ta, tb = SG_LAYOUT[lay]
     M = N = K = 4096
-    say("sgemm baseline", lay)
+    splits = hk.lib().hk_sgemm_split_count(enum, M, N, K, 1, split_k)
+    say("sgemm baseline", lay, "split_k", split_k, "splits", splits)
+    if split_k:
+        assert splits == split_k
     A, B, C0, bias = _sg_operands(orc, M, N, K, ta, tb, 140, normal=True)
     out = _sg_call(hk, "hk_sgemm", enum, torch.from_numpy(A).to(DEV), torch.from_numpy(B).to(DEV),
                    torch.from_numpy(C0).to(DEV), M, N, K, 1.0, 1.0,
-                   bias=torch.from_numpy(bias).to(DEV), bias_stride=N, split_k=4)
+                   bias=torch.from_numpy(bias).to(DEV), bias_stride=N, split_k=split_k)
     rows = np.unique(np.concatenate([np.arange(0, M, 67), [M - 1]]))
     Asub = np.ascontiguousarray(A[:, rows] if ta else A[rows, :])
     ref = orc.sgemm(ta, tb, Asub, B, alpha=1.0, beta=1.0, C0=np.ascontiguousarray(C0[rows]),
@@ -365,6 +432,33 @@ def test_sgemm_baseline_shape_split_k4_sampled_rows(hk, orc, lay):
     rel = max_rel(out[rows], ref)
     print(f"sgemm baseline rel {rel:.2e}")
     assert rel <= 2e-3
+
+
+@pytest.mark.parametrize("split_k", [1, 3])
+def test_sgemm_infinite_operand(hk, orc, split_k):
+    # An inf in A reaches the outputs of its row as +-inf, as it does through the reference's
+    # TF32 products and the oracle's fp32 loop. The bf16x3 split keeps the inf in the high part
+    # and zeroes its low part and its copy in the cross term; without that, inf * b_lo (NaN for
+    # b_lo = 0 or of the other sign) and bf16(inf - inf) would turn the row into NaN.
+    M, N, K = 64, 128, 96
+    say("sgemm inf operand", split_k)
+    A, B, C0, _ = _sg_operands(orc, M, N, K, 0, 0, 150)
+    A = A.copy()
+    A[3, 5] = np.inf
+    A[7, 9] = -np.inf
+    A[11, 2] = np.float32(3.4e38)  # finite, but rounds to bf16 inf: treated as inf
+    assert hk.lib().hk_sgemm_split_count(2, M, N, K, 1, split_k) == split_k
+    out = _sg_call(hk, "hk_sgemm", 2, torch.from_numpy(A).to(DEV), torch.from_numpy(B).to(DEV),
+                   torch.from_numpy(C0).to(DEV), M, N, K, 1.0, 0.5, split_k=split_k)
+    ref = orc.sgemm(0, 0, A, B, alpha=1.0, beta=0.5, C0=C0)
+    for r in (3, 7):
+        assert np.isinf(ref[r]).all()
+        np.testing.assert_array_equal(out[r], ref[r])
+    # the 3e38 row: the GPU's hi * b terms are +-inf where the oracle's exact fp32 products may
+    # stay finite; what must not appear is NaN
+    assert not np.isnan(out[11]).any()
+    finite = np.setdiff1d(np.arange(M), [3, 7, 11])
+    assert max_rel(out[finite], ref[finite]) <= 2e-3
 
 
 def test_bgemm_split_k_on_concurrent_streams(hk, orc):
