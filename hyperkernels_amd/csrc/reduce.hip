@@ -20,6 +20,8 @@
 //   generic: a wave per output; each lane walks the reduced index space with the strided
 //            offset map.
 #include <algorithm>
+#include <mutex>
+#include <vector>
 
 #include "hk_device.h"
 #include "hk_host.h"
@@ -187,8 +189,28 @@ hipError_t finalize(const float* part, float* dst, int64_t nout, int split, hipS
 // Workgroups wanted in flight to cover the device: 2 per CU.
 int64_t target_groups() { return static_cast<int64_t>(hk::device_cu_count()) * 2; }
 
+// Where a split reduction keeps its partials [split][num_outputs]: the library's grow-only
+// workspace of the stream (scratch == nullptr), or a fixed scratch array of `scratch_bytes`
+// (the entry point that allocates nothing), which a plan needing more bytes is refused.
+struct PartialSource {
+  float* scratch = nullptr;
+  size_t scratch_bytes = 0;
+
+  hipError_t get(size_t bytes, hipStream_t stream, float** out) const {
+    if (scratch) {
+      if (bytes > scratch_bytes) return hipErrorInvalidValue;
+      *out = scratch;
+      return hipSuccess;
+    }
+    void* ws = nullptr;
+    HK_RETURN_IF_ERROR(hk::device_workspace(bytes, stream, &ws));
+    *out = static_cast<float*>(ws);
+    return hipSuccess;
+  }
+};
+
 hipError_t reduce_inner(const float* src, float* dst, int64_t nout, int64_t len,
-                        int64_t row_stride, hipStream_t stream) {
+                        int64_t row_stride, const PartialSource& ps, hipStream_t stream) {
   if (len < 1024) {
     hipLaunchKernelGGL(reduce_inner_wave, dim3(static_cast<unsigned>(hk::ceil_div(nout, kWaves))),
                        dim3(kThreads), 0, stream, src, dst, row_stride, len, nout);
@@ -205,11 +227,8 @@ hipError_t reduce_inner(const float* src, float* dst, int64_t nout, int64_t len,
   const int64_t slice_len = hk::ceil_div(hk::ceil_div(len, split), 4) * 4;
   split = hk::ceil_div(len, slice_len);
   float* out = dst;
-  if (split > 1) {
-    void* ws = nullptr;
-    HK_RETURN_IF_ERROR(hk::device_workspace(static_cast<size_t>(split * nout) * sizeof(float), stream, &ws));
-    out = static_cast<float*>(ws);
-  }
+  if (split > 1)
+    HK_RETURN_IF_ERROR(ps.get(static_cast<size_t>(split * nout) * sizeof(float), stream, &out));
   hipLaunchKernelGGL(reduce_inner_block, dim3(static_cast<unsigned>(nout), static_cast<unsigned>(split)),
                      dim3(kBlockThreads), 0, stream, src, out, row_stride, len, slice_len, nout);
   HK_RETURN_IF_ERROR(hk::launch_status());
@@ -219,7 +238,7 @@ hipError_t reduce_inner(const float* src, float* dst, int64_t nout, int64_t len,
 
 hipError_t reduce_outer_launch(const float* src, float* dst, int64_t nout, int64_t inner,
                                int64_t outer_stride, int64_t row_stride, int64_t len,
-                               hipStream_t stream) {
+                               const PartialSource& ps, hipStream_t stream) {
   const int64_t gx = hk::ceil_div(nout, kThreads);
   int64_t split = 1;
   if (gx < target_groups() * 2) {
@@ -230,11 +249,8 @@ hipError_t reduce_outer_launch(const float* src, float* dst, int64_t nout, int64
   const int64_t slice_len = hk::ceil_div(len, split);
   split = hk::ceil_div(len, slice_len);
   float* out = dst;
-  if (split > 1) {
-    void* ws = nullptr;
-    HK_RETURN_IF_ERROR(hk::device_workspace(static_cast<size_t>(split * nout) * sizeof(float), stream, &ws));
-    out = static_cast<float*>(ws);
-  }
+  if (split > 1)
+    HK_RETURN_IF_ERROR(ps.get(static_cast<size_t>(split * nout) * sizeof(float), stream, &out));
   hipLaunchKernelGGL(reduce_outer, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(split)),
                      dim3(kThreads), 0, stream, src, out, nout, inner, outer_stride, row_stride,
                      len, slice_len);
@@ -254,11 +270,34 @@ hipError_t zero_outputs(float* dst, int64_t nout, hipStream_t stream) {
   return hk::launch_status();
 }
 
-}  // namespace
+// Scratch of the entry point that allocates nothing (hk_unified_reduce_sum_f32_noalloc): the
+// split partials [split][num_outputs] of one call, at most kScratchBytes. Each device holds
+// its own copy for the life of the process. Every slot a call uses is written by that call's
+// first kernel before its finalize reads it, so nothing needs clearing; calls that overlap on
+// one device share the array and race.
+constexpr size_t kScratchBytes = HK_REDUCE_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
-extern "C" hipError_t hk_unified_reduce_sum_f32(const hk_reduction_layout* layout,
-                                                const float* src, float* dst,
-                                                hipStream_t stream) {
+// Device address of `scratch` on the current device, looked up once per device with that
+// device current (the host-side name is only a stand-in for the symbol, not an address).
+hipError_t scratch_address(float** out) {
+  static std::mutex mu;
+  static std::vector<float*> addr;
+  int dev = 0;
+  HK_RETURN_IF_ERROR(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(mu);
+  if (static_cast<int>(addr.size()) <= dev) addr.resize(dev + 1, nullptr);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    HK_RETURN_IF_ERROR(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    addr[dev] = static_cast<float*>(p);
+  }
+  *out = addr[dev];
+  return hipSuccess;
+}
+
+hipError_t unified_reduce(const hk_reduction_layout* layout, const float* src, float* dst,
+                          const PartialSource& ps, hipStream_t stream) {
   HK_CHECK_ARG(layout != nullptr);
   const hk_reduction_layout& L = *layout;
   HK_CHECK_ARG(L.num_outputs >= 0 && L.reduced_count >= 0);
@@ -269,13 +308,13 @@ extern "C" hipError_t hk_unified_reduce_sum_f32(const hk_reduction_layout* layou
   switch (L.path) {
     case HK_REDUCE_INNER: {
       const int64_t row_stride = L.input_outer_stride > 0 ? L.input_outer_stride : L.reduced_count;
-      return reduce_inner(src, dst, L.num_outputs, L.reduced_count, row_stride, stream);
+      return reduce_inner(src, dst, L.num_outputs, L.reduced_count, row_stride, ps, stream);
     }
     case HK_REDUCE_OUTER: {
       const int64_t inner = L.inner_count > 0 ? L.inner_count : L.num_outputs;
       HK_CHECK_ARG(L.input_row_stride > 0);
       return reduce_outer_launch(src, dst, L.num_outputs, inner, L.input_outer_stride,
-                                 L.input_row_stride, L.reduced_count, stream);
+                                 L.input_row_stride, L.reduced_count, ps, stream);
     }
     case HK_REDUCE_GENERIC: {
       // A layout-only generic request describes contiguous rows (the reference self-test's
@@ -289,6 +328,23 @@ extern "C" hipError_t hk_unified_reduce_sum_f32(const hk_reduction_layout* layou
     default:
       return hipErrorInvalidValue;
   }
+}
+
+}  // namespace
+
+extern "C" hipError_t hk_unified_reduce_sum_f32(const hk_reduction_layout* layout,
+                                                const float* src, float* dst,
+                                                hipStream_t stream) {
+  return unified_reduce(layout, src, dst, PartialSource{}, stream);
+}
+
+extern "C" hipError_t hk_unified_reduce_sum_f32_noalloc(const hk_reduction_layout* layout,
+                                                        const float* src, float* dst,
+                                                        hipStream_t stream) {
+  PartialSource ps;
+  HK_RETURN_IF_ERROR(scratch_address(&ps.scratch));
+  ps.scratch_bytes = kScratchBytes;
+  return unified_reduce(layout, src, dst, ps, stream);
 }
 
 extern "C" hipError_t hk_reduce_generic_f32(const float* src, float* dst, int out_ndim,

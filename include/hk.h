@@ -250,6 +250,20 @@ typedef struct hk_reduction_layout {
 
 HK_API hipError_t hk_unified_reduce_sum_f32(const hk_reduction_layout* layout, const float* src,
                                      float* dst, hipStream_t stream);
+/* hk_unified_reduce_sum_f32 without any allocation. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, plan and results (bit for bit) as
+ * hk_unified_reduce_sum_f32; the split partials live in a fixed array of
+ * HK_REDUCE_NOALLOC_SCRATCH_BYTES that each device holds for the life of the process, instead
+ * of the stream's grow-only workspace. The size covers every plan on a 256-CU device (the
+ * largest, an outer-axis split, needs 2,096,128 bytes); a plan whose partials need more (split
+ * count x num_outputs x 4 bytes, possible on a device with more CUs) returns
+ * hipErrorInvalidValue before anything is launched. Calls that overlap on one device share the
+ * array: they must be ordered (one stream, or events between streams). */
+#define HK_REDUCE_NOALLOC_SCRATCH_BYTES (2u << 20)
+HK_API hipError_t hk_unified_reduce_sum_f32_noalloc(const hk_reduction_layout* layout,
+                                                    const float* src, float* dst,
+                                                    hipStream_t stream);
 #define HK_REDUCE_MAX_DIMS 10
 HK_API hipError_t hk_reduce_generic_f32(const float* src, float* dst, int out_ndim,
                                  const int64_t* out_sizes, const int64_t* out_strides,
