@@ -40,6 +40,7 @@
 // Shapes the tiled kernel does not take (a contiguous extent or leading dimension that is not
 // a multiple of 8, pointers not 16-byte aligned) run on a simple fp32-accumulating kernel.
 #include <mutex>
+#include <type_traits>
 
 #include "hk_device.h"
 #include "hk_host.h"
@@ -305,7 +306,7 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
   const bool tail = (klen % BK) != 0;  // last k-tile is partial
 
   // Copy q (0 .. 2 * kLoadsPerWave - 1) of k-tile kt into ring slot `slot`. On a partial last
-  // k-tile, lanes whose 8 k values lie past the split's end store zeros instead.
+  // k-tile (fill), lanes whose 8 k values lie past the split's end store zeros instead.
   auto copy = [&](int kt, int slot, int q, bool fill) {
     const bool isA = q < kLoadsPerWave;
     const int i = isA ? q : q - kLoadsPerWave;
@@ -351,7 +352,13 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
   constexpr int kReadsPerStep = (A_KMAJOR ? 1 : 2) * kBlkM + (B_KMAJOR ? 1 : 2) * kBlkN;
   constexpr int kMfmaPerStep = kBlkM * kBlkN;
 
-  for (int kt = 0; kt < ktiles; ++kt) {
+  // One k-tile. STEADY (compile-time): tile kt + kStages exists and is whole, so its 32 copies
+  // are issued with no per-copy condition; otherwise whether it exists (more) and whether it is
+  // the partial last k-tile (fill) are tested at run time.
+  auto ktile = [&](int kt, auto steady_tag) {
+    constexpr bool STEADY = decltype(steady_tag)::value;
+    const bool more = STEADY || kt + kStages < ktiles;
+    const bool fill = !STEADY && tail && kt + kStages == ktiles - 1;
     const int slot = kt & 1;
     const unsigned char HK_LDS* sa = ldsA + slot * kStageBytes;
     const unsigned char HK_LDS* sb = ldsB + slot * kStageBytes;
@@ -381,8 +388,6 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
 #pragma unroll
           for (int j = 0; j < kBlkN; ++j) fb[nxt][j] = OB::read(nb, wn * kWaveN, j, 0, lane);
         }
-        const bool more = kt + kStages < ktiles;
-        const bool fill = tail && kt + kStages == ktiles - 1;
 #pragma unroll
         for (int i = 0; i < kBlkM; ++i)
 #pragma unroll
@@ -391,14 +396,23 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
                                                                 acc[i][j], 0, 0, 0);
             const int q = i * kBlkN + j;
             if (more && q < kCopies) copy(kt + kStages, slot, q, fill);
+            // steady state: keep each copy next to its MFMA, so that a wave's copies are spread
+            // over the step (the copies are inline asm, which the scheduler does not group)
+            if constexpr (STEADY) __builtin_amdgcn_sched_barrier(0);
           }
         if (kCopies > kMfmaPerStep && more) {
 #pragma unroll
           for (int q = kMfmaPerStep; q < kCopies; ++q) copy(kt + kStages, slot, q, fill);
         }
+
       }
     }
-  }
+  };
+  // steady state: every k-tile kt < steady has a whole k-tile kt + kStages to copy
+  const int steady = ktiles - kStages - (tail ? 1 : 0);
+  int kt = 0;
+  for (; kt < steady; ++kt) ktile(kt, std::true_type{});
+  for (; kt < ktiles; ++kt) ktile(kt, std::false_type{});
 
   // Epilogue. Lane l holds, for MFMA block (i, j) and quad q, output row
   // wm*128 + 32 i + l % 32 and columns wn*128 + 32 j + 8 q + 4 (l / 32) .. +3.

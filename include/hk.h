@@ -423,6 +423,7 @@ HK_API int hk_sgemm_split_count(int layout, int M, int N, int K, int batchCount,
  * split on the bf16 MFMA (fp32-class accuracy, relative error ~1e-5; gfx950 has no TF32 MFMA).
  * Tensors are [B, nh, T, head_dim] with arbitrary batch/head/row strides (elements; last-dim
  * stride 1; strides multiples of 4 and 16-byte aligned bases), LSE and D are [B, nh, T].
+ * Non-finite inputs give NaN outputs.
  * The parameter blocks repeat the reference's field order and types exactly:
  *   hk_attn_fwd_params = MemEfficientFwdParams
  *     (kernels/attention/fused_attn_forward_kernel_tc_sm89.cu:8-29);
