@@ -364,7 +364,7 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
     float mt = sc[0];
 #pragma unroll
     for (int i = 1; i < 16; ++i) mt = fmaxf(mt, sc[i]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32, HK_WAVE));
+    mt = hk::half32_reduce(mt, hk::MaxOp{});
     // The reference moves on the query's first tile with an unmasked score, and when a score
     // exceeds it by more than kTau; otherwise (most tiles) it stays.
     const bool first = m == -INFINITY;
@@ -448,7 +448,7 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
     __syncthreads();
   }
 
-  const float lt = l + __shfl_xor(l, 32, HK_WAVE);
+  const float lt = hk::half32_reduce(l, hk::AddOp{});
   if (q < T) {
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     float* orow = Ob + q * p.o_strideM;
@@ -484,8 +484,7 @@ __global__ __launch_bounds__(256) void attn_precompute_d_kernel(hk_attn_bwd_para
       s += (a.x * g.x + a.y * g.y) + (a.z * g.z + a.w * g.w);
     }
   }
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 16);
+  s = hk::row16_sum(s);
   if (row < p.T && sub == 0) p.D[b * p.d_strideB + h * p.d_strideH + row] = s;
 }
 
@@ -501,8 +500,7 @@ __global__ __launch_bounds__(256) void attn_precompute_d_scalar(hk_attn_bwd_para
     const float* d = p.dO + b * p.do_strideB + h * p.do_strideH + row * p.do_strideM;
     for (int k = sub; k < hd; k += 16) s += o[k] * d[k];
   }
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 16);
+  s = hk::row16_sum(s);
   if (row < p.T && sub == 0) p.D[b * p.d_strideB + h * p.d_strideH + row] = s;
 }
 

@@ -112,8 +112,8 @@ __global__ __launch_bounds__(kThreads) void gemv_dot(int R, int K, int kchunk,
         acc += hk::bf16_to_f32(row[k]) * hk::bf16_to_f32(xb[k * incx]);
     }
   }
-#pragma unroll
-  for (int off = kDotLanes / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kDotLanes);
+  static_assert(kDotLanes == 16, "the dot form sums each row over one 16-lane DPP row");
+  acc = hk::row16_sum(acc);
   if (r < R && j == 0) emit(out, b, s, R, r, acc);
 }
 

@@ -119,16 +119,55 @@ __device__ __forceinline__ float tree_sum(const float* f) {
   }
 }
 
-// ---- wave reductions (64 lanes, butterfly: every lane ends with the result) ----------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, HK_WAVE);
-  return v;
+// ---- wave reductions (every lane ends with the result) --------------------------------------
+// A butterfly held in registers: within each row of 16 lanes the partner values come through
+// DPP (quad_perm [1,0,3,2] and [2,3,0,1], i.e. lane ^ 1 and lane ^ 2, then row_half_mirror,
+// lane i <-> 7 - i, and row_mirror, lane i <-> 15 - i), and the four rows are combined with
+// gfx950's v_permlane16_swap and v_permlane32_swap, which called with (v, v) return the even
+// and the odd row (then the lower and the upper 32 lanes) side by side. Every step pairs
+// lanes symmetrically, so with a commutative `op` all lanes end with the same bits; nothing
+// goes through LDS (a ds_bpermute butterfly costs six LDS round trips).
+namespace detail {
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, HK_WAVE));
-  return v;
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+}  // namespace detail
+
+// op over the 16 lanes of each row (lanes 16r .. 16r + 15)
+template <typename Op>
+__device__ __forceinline__ float row16_reduce(float v, Op op) {
+  v = op(v, detail::dpp<detail::kDppXor1>(v));
+  v = op(v, detail::dpp<detail::kDppXor2>(v));
+  v = op(v, detail::dpp<detail::kDppHalfMirror>(v));
+  return op(v, detail::dpp<detail::kDppMirror>(v));
+}
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+  v = row16_reduce(v, op);
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return op(__uint_as_float(h[0]), __uint_as_float(h[1]));
+}
+struct AddOp {
+  __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct MaxOp {
+  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+__device__ __forceinline__ float wave_sum(float v) { return wave_reduce(v, AddOp{}); }
+__device__ __forceinline__ float wave_max(float v) { return wave_reduce(v, MaxOp{}); }
+__device__ __forceinline__ float row16_sum(float v) { return row16_reduce(v, AddOp{}); }
+// op of lane l's value with lane l ^ 32's (one v_permlane32_swap)
+template <typename Op>
+__device__ __forceinline__ float half32_reduce(float v, Op op) {
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return op(__uint_as_float(h[0]), __uint_as_float(h[1]));
 }
 
 // ---- (max, sum-of-exp) pair used by the streaming softmax ----------------------------------
@@ -139,13 +178,22 @@ __device__ __forceinline__ void softmax_merge(float& m, float& s, float m2, floa
   s = s * __expf(m - mn) + s2 * __expf(m2 - mn);
   m = mn;
 }
+// The same register butterfly as wave_reduce over (m, s) pairs; softmax_merge is symmetric in
+// its two states, so every lane ends with the same pair.
 __device__ __forceinline__ void wave_softmax_merge(float& m, float& s) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float m2 = __shfl_xor(m, off, HK_WAVE);
-    const float s2 = __shfl_xor(s, off, HK_WAVE);
-    softmax_merge(m, s, m2, s2);
-  }
+  auto step = [&](float m2, float s2) { softmax_merge(m, s, m2, s2); };
+  step(detail::dpp<detail::kDppXor1>(m), detail::dpp<detail::kDppXor1>(s));
+  step(detail::dpp<detail::kDppXor2>(m), detail::dpp<detail::kDppXor2>(s));
+  step(detail::dpp<detail::kDppHalfMirror>(m), detail::dpp<detail::kDppHalfMirror>(s));
+  step(detail::dpp<detail::kDppMirror>(m), detail::dpp<detail::kDppMirror>(s));
+  auto swap_step = [&](auto sw) {
+    const auto pm = sw(__float_as_uint(m)), ps = sw(__float_as_uint(s));
+    m = __uint_as_float(pm[0]);
+    s = __uint_as_float(ps[0]);
+    softmax_merge(m, s, __uint_as_float(pm[1]), __uint_as_float(ps[1]));
+  };
+  swap_step([](uint32_t v) { return __builtin_amdgcn_permlane16_swap(v, v, false, false); });
+  swap_step([](uint32_t v) { return __builtin_amdgcn_permlane32_swap(v, v, false, false); });
 }
 
 __host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) {

@@ -107,6 +107,15 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_reg(const uint4* __restrict__
   }
 }
 
+// Waves per workgroup of the backward kernels that accumulate gamma/beta: 8 when the flat
+// LDS reduction of 8 waves fits 64 KiB (cols <= 1024), else 4. The grid is one workgroup
+// per CU (8 waves) or two (4 waves), so each CU holds 8 waves and writes one or two partials
+// for the finalize to read back. Measured at 4096 x 768 on MI355X against 4 waves and two
+// workgroups per CU (512 partials): 12.2 against 12.9 us per fused backward (fp32), 9.8
+// against 10.7 us (bf16); 16 waves per workgroup with one row per wave, and a tree
+// reduction over the waves instead of the flat one, were both slower.
+constexpr int gb_waves(int cols) { return cols <= 1024 ? 8 : 4; }
+
 // ------------------------------------------------------------------------------------------
 // Backward, register-resident rows. WRITE_DX: produce grad_x. DO_GB: accumulate the
 // per-workgroup gamma/beta partials into part[blockIdx.x][2 * cols] (gamma then beta).
@@ -114,8 +123,8 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_reg(const uint4* __restrict__
 // so the two wave reductions of one row overlap the loads of the next. dy, x and gamma stay
 // in registers in their storage format and are widened to fp32 where they are used.
 // ------------------------------------------------------------------------------------------
-template <typename T, int VPL, bool WRITE_DX, bool DO_GB>
-__global__ __launch_bounds__(kThreads) void ln_bwd_reg(
+template <typename T, int VPL, bool WRITE_DX, bool DO_GB, int WAVES>
+__global__ __launch_bounds__(WAVES * HK_WAVE) void ln_bwd_reg(
     const uint4* __restrict__ dy, const uint4* __restrict__ x, const float* __restrict__ mean,
     const float* __restrict__ rstd, const uint4* __restrict__ gamma, uint4* __restrict__ dx,
     float* __restrict__ part, int rows, int nvec, float inv_cols) {
@@ -123,7 +132,7 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_reg(
   // row whose terms cancel exactly (cols == 1) gives exactly zero.
 #pragma clang fp contract(off)
   constexpr int P = T::kPerVec;
-  extern __shared__ float4 lds4[];  // [kWavesPerBlock][2][cols] floats when DO_GB
+  extern __shared__ float4 lds4[];  // [WAVES][2][cols] floats when DO_GB
   const int lane = threadIdx.x & (HK_WAVE - 1);
   const int wave = threadIdx.x >> 6;
   uint4 graw[VPL];
@@ -135,8 +144,8 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_reg(
 #pragma unroll
     for (int k = 0; k < P; ++k) acc_g[i][k] = acc_b[i][k] = 0.f;
   }
-  const int stride = gridDim.x * kWavesPerBlock;
-  int row = blockIdx.x * kWavesPerBlock + wave;
+  const int stride = gridDim.x * WAVES;
+  int row = blockIdx.x * WAVES + wave;
   uint4 dn[VPL], xn[VPL];
   float mn = 0.f, rn = 0.f;
   auto fetch = [&](int r) {
@@ -235,10 +244,10 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_reg(
     }
     __syncthreads();
     float4* out = reinterpret_cast<float4*>(part) + static_cast<int64_t>(blockIdx.x) * 2 * cols4;
-    for (int c = threadIdx.x; c < 2 * cols4; c += kThreads) {
+    for (int c = threadIdx.x; c < 2 * cols4; c += WAVES * HK_WAVE) {
       float4 s = lds4[c];
 #pragma unroll
-      for (int w = 1; w < kWavesPerBlock; ++w) {
+      for (int w = 1; w < WAVES; ++w) {
         const float4 t = lds4[static_cast<int64_t>(w) * 2 * cols4 + c];
         s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
       }
@@ -248,32 +257,36 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_reg(
 }
 
 // Sums nparts partials [nparts][2 * cols] in a fixed order and adds them into grad_gamma /
-// grad_beta. A workgroup of 16 waves owns 64 columns: wave w sums partials w, w + 16, ...
-// (eight loads in flight per lane), then the 16 wave sums are added in wave order in LDS.
-constexpr int kFinWaves = 16;
-__global__ __launch_bounds__(kFinWaves * HK_WAVE) void ln_gb_finalize(
+// grad_beta. A workgroup owns kFinCols columns and spreads the partials over kFinGroups lane
+// groups: group g sums partials g, g + kFinGroups, ... (eight loads in flight per lane, one
+// round for up to 256 partials), then the group sums are added in group order in LDS. Narrow
+// column slices spread the read of the partials over 2 x cols / 16 workgroups.
+constexpr int kFinCols = 16;
+constexpr int kFinGroups = 32;
+__global__ __launch_bounds__(kFinCols * kFinGroups) void ln_gb_finalize(
     const float* __restrict__ part, int nparts, int cols, float* __restrict__ grad_gamma,
     float* __restrict__ grad_beta) {
-  __shared__ float red[kFinWaves][HK_WAVE];
-  const int lane = threadIdx.x & (HK_WAVE - 1);
-  const int wave = threadIdx.x >> 6;
-  const int c = blockIdx.x * HK_WAVE + lane;
+  __shared__ float red[kFinGroups][kFinCols];
+  const int col = threadIdx.x % kFinCols;
+  const int grp = threadIdx.x / kFinCols;
+  const int c = blockIdx.x * kFinCols + col;
   const int width = 2 * cols;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (c < width) {
-    int p = wave;
-    for (; p + 7 * kFinWaves < nparts; p += 8 * kFinWaves) {
+    int p = grp;
+    for (; p + 7 * kFinGroups < nparts; p += 8 * kFinGroups) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc[u] += part[static_cast<int64_t>(p + u * kFinWaves) * width + c];
+      for (int u = 0; u < 8; ++u)
+        acc[u] += part[static_cast<int64_t>(p + u * kFinGroups) * width + c];
     }
-    for (; p < nparts; p += kFinWaves) acc[0] += part[static_cast<int64_t>(p) * width + c];
+    for (; p < nparts; p += kFinGroups) acc[0] += part[static_cast<int64_t>(p) * width + c];
   }
-  red[wave][lane] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  red[grp][col] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
-  if (wave == 0 && c < width) {
-    float s = red[0][lane];
+  if (grp == 0 && c < width) {
+    float s = red[0][col];
 #pragma unroll
-    for (int w = 1; w < kFinWaves; ++w) s += red[w][lane];
+    for (int g = 1; g < kFinGroups; ++g) s += red[g][col];
     if (c < cols) {
       if (grad_gamma) grad_gamma[c] += s;
     } else {
@@ -416,9 +429,10 @@ constexpr int kMaxGbCols = 2048;
 template <typename T>
 constexpr int kMaxBwdVpl = 4096 / (HK_WAVE * T::kPerVec);
 
-int bwd_grid(int rows) {
-  const int64_t want = hk::ceil_div(rows, kWavesPerBlock);
-  const int64_t cap = static_cast<int64_t>(hk::device_cu_count()) * 2;
+// Workgroups of a gamma/beta backward: one per `waves` rows, at most 8 / waves per CU.
+int bwd_gb_grid(int rows, int waves) {
+  const int64_t want = hk::ceil_div(rows, waves);
+  const int64_t cap = static_cast<int64_t>(hk::device_cu_count()) * (8 / waves);
   return static_cast<int>(want < cap ? want : cap);
 }
 
@@ -455,15 +469,16 @@ hipError_t launch_bwd(const St<T>* dy, const St<T>* x, const float* mean, const 
   if (rows == 0 || cols == 0) return hipSuccess;
   HK_CHECK_ARG(dy && x && mean && rstd);
   HK_CHECK_ARG(!write_dx || dx);
-  // The gamma/beta partials of one workgroup live in LDS: 4 waves x 2 x cols floats, kept
-  // within 64 KiB (cols <= kMaxGbCols). The backward keeps dy, x and their prefetch in
+  // The gamma/beta partials of one workgroup live in LDS: 8 (cols <= 1024) or 4 waves x 2 x
+  // cols floats, kept within 64 KiB (cols <= kMaxGbCols). The backward keeps dy, x and their prefetch in
   // registers; past kMaxBwdVpl vectors per lane (4096 columns for every storage type) it would
   // spill, so wider rows take the workgroup-per-row kernels.
   if (reg_path_ok<T>(cols, {dy, x, gamma, dx}) && pick_vpl(cols / T::kPerVec) <= kMaxBwdVpl<T> &&
       (!do_gb || cols <= kMaxGbCols)) {
     const int nvec = cols / T::kPerVec;
-    const int grid = write_dx && !do_gb ? static_cast<int>(hk::ceil_div(rows, kWavesPerBlock))
-                                        : bwd_grid(rows);
+    const int waves = do_gb ? gb_waves(cols) : kWavesPerBlock;
+    const int grid = do_gb ? bwd_gb_grid(rows, waves)
+                           : static_cast<int>(hk::ceil_div(rows, kWavesPerBlock));
     float* part = nullptr;
     if (do_gb) {
       void* ws = nullptr;
@@ -471,7 +486,7 @@ hipError_t launch_bwd(const St<T>* dy, const St<T>* x, const float* mean, const 
           hk::device_workspace(static_cast<size_t>(grid) * 2 * cols * sizeof(float), stream, &ws));
       part = static_cast<float*>(ws);
     }
-    const size_t lds = do_gb ? static_cast<size_t>(kWavesPerBlock) * 2 * cols * sizeof(float) : 0;
+    const size_t lds = do_gb ? static_cast<size_t>(waves) * 2 * cols * sizeof(float) : 0;
     const float inv_cols = 1.0f / static_cast<float>(cols);
     HK_RETURN_IF_ERROR(with_vpl(pick_vpl(nvec), [&](auto vpl_c) -> hipError_t {
       constexpr int V = decltype(vpl_c)::value;
@@ -479,14 +494,22 @@ hipError_t launch_bwd(const St<T>* dy, const St<T>* x, const float* mean, const 
       if constexpr (V > kMaxBwdVpl<T>) {
         return hipErrorInvalidValue;
       } else {
-        constexpr bool kGb = V * HK_WAVE * T::kPerVec <= kMaxGbCols;
-        void (*k)(const uint4*, const uint4*, const float*, const float*, const uint4*, uint4*,
-                  float*, int, int, float) = ln_bwd_reg<T, V, true, false>;
+        constexpr int kCols = V * HK_WAVE * T::kPerVec;  // the widest row of this VPL
+        constexpr bool kGb = kCols <= kMaxGbCols;
+        using Kernel = void (*)(const uint4*, const uint4*, const float*, const float*,
+                                const uint4*, uint4*, float*, int, int, float);
+        Kernel k = ln_bwd_reg<T, V, true, false, kWavesPerBlock>;
+        // pick_vpl takes the smallest VPL that holds the row, so cols <= 1024 exactly when
+        // kCols <= 1024: the wave count of the gamma/beta forms is fixed by V
+        constexpr int kW = gb_waves(kCols);
         if constexpr (kGb) {
-          if (do_gb) k = write_dx ? ln_bwd_reg<T, V, true, true> : ln_bwd_reg<T, V, false, true>;
+          if (do_gb) {
+            if (waves != kW) return hipErrorInvalidValue;
+            k = write_dx ? ln_bwd_reg<T, V, true, true, kW> : ln_bwd_reg<T, V, false, true, kW>;
+          }
         }
         if (do_gb && !kGb) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), lds, stream,
+        hipLaunchKernelGGL(k, dim3(grid), dim3(waves * HK_WAVE), lds, stream,
                            reinterpret_cast<const uint4*>(dy), reinterpret_cast<const uint4*>(x),
                            mean, rstd, reinterpret_cast<const uint4*>(gamma),
                            reinterpret_cast<uint4*>(dx), part, rows, nvec, inv_cols);
@@ -494,8 +517,9 @@ hipError_t launch_bwd(const St<T>* dy, const St<T>* x, const float* mean, const 
       }
     }));
     if (do_gb) {
-      hipLaunchKernelGGL(ln_gb_finalize, dim3(static_cast<unsigned>(hk::ceil_div(2 * cols, HK_WAVE))),
-                         dim3(kFinWaves * HK_WAVE), 0, stream, part, grid, cols, dgamma, dbeta);
+      hipLaunchKernelGGL(ln_gb_finalize,
+                         dim3(static_cast<unsigned>(hk::ceil_div(2 * cols, kFinCols))),
+                         dim3(kFinCols * kFinGroups), 0, stream, part, grid, cols, dgamma, dbeta);
       HK_RETURN_IF_ERROR(hk::launch_status());
     }
     return hipSuccess;

@@ -499,6 +499,19 @@ HK_API hipError_t hk_attn_bwd_precompute_D(const hk_attn_bwd_params* params, int
 HK_API hipError_t hk_attn_backward(const hk_attn_bwd_params* params, int head_dim,
                                    hipStream_t stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Measurement
+ * ---------------------------------------------------------------------------------------- */
+/* HBM stream with a given read/write mix. No counterpart in the reference: a measurement aid for
+ * benchmarks, which time it to find the HBM rate a memory-bound kernel's mix can reach. Reads
+ * n_in (0-4) fp32 arrays in[s] of n elements and writes n_out (0-3) arrays out[s] of n elements,
+ * out[s][i] = sum over inputs of in[.][i] + s. n is a multiple of 4, every array 16-byte
+ * aligned; each workgroup covers `unroll` (1, 2 or 4) spans of 256 x 16 bytes per array. With
+ * n_out == 0, `sink` (one float per workgroup) must be non-NULL; it is written only if an
+ * element sum equals 1234.5. The pointer arrays are read on the host. */
+HK_API hipError_t hk_hbm_stream(const float* const* in, int n_in, float* const* out, int n_out,
+                                int64_t n, int unroll, float* sink, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

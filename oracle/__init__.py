@@ -46,6 +46,7 @@ class _NullableU16(object):
 _SIGS = {
     "oracle_set_threads": (None, [_i]),
     "oracle_max_threads": (_i, []),
+    "oracle_hardware_concurrency": (_i, []),
     "oracle_f32_to_bf16": (None, [_f32p, _u16p, _i64]),
     "oracle_bf16_to_f32": (None, [_u16p, _f32p, _i64]),
     "oracle_rand_uniform": (None, [_f32p, _i64, _u64, _f, _f]),
@@ -108,6 +109,11 @@ def set_threads(n: int) -> None:
 
 def max_threads() -> int:
     return lib().oracle_max_threads()
+
+
+def hardware_concurrency() -> int:
+    """std::thread::hardware_concurrency() of this host (hardware threads, not the affinity)."""
+    return lib().oracle_hardware_concurrency()
 
 
 # ---- conversions and generators ----------------------------------------------------------------

@@ -21,6 +21,7 @@
 #include <cmath>
 #include <cstring>
 #include <random>
+#include <thread>
 #include <vector>
 
 #define ORACLE_API extern "C" __attribute__((visibility("default")))
@@ -71,6 +72,9 @@ inline float tanh_gelu_grad(float x) {
 // ---------------------------------------------------------------------------------------------
 ORACLE_API void oracle_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
 ORACLE_API int oracle_max_threads(void) { return omp_get_max_threads(); }
+ORACLE_API int oracle_hardware_concurrency(void) {
+  return static_cast<int>(std::thread::hardware_concurrency());
+}
 
 ORACLE_API void oracle_f32_to_bf16(const float* in, uint16_t* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = f32_to_bf16(in[i]);
