@@ -9,14 +9,21 @@ tensors (124,439,808 fp32 parameters), in that order so that no kernel finds its
 time (GB/s, the reference's byte conventions, README.md:186-199).
 
 `roofline` is for the step's dominant kernel (longest average duration), timed live with HIP
-events on the launch stream. `cpu_baseline` is the repository's CPU oracle (a restatement of
-the reference harnesses' CPU references) timed on this host on a bounded sample of the same
-step. `per_kernel` lists each kernel of the surface at its BASELINE config, timed alone: each
-repetition flushes the caches and times one burst of launches between one pair of events
-(memory-bound kernels: one launch per distinct buffer set, ~1 GiB touched in all, so every
-launch reads HBM; compute-bound kernels: 5 launches of the same operands).
+events on the launch stream; its `mix_ceiling` is the rate hk_hbm_stream reaches with the same
+read/write mix and byte count (AdamW: 4 arrays in, 3 out). `cpu_baseline` is the repository's
+CPU oracle (a restatement of the reference harnesses' CPU references) timed on this host on a
+bounded sample of the same step, on every core the host gives the process and on one thread.
+`per_kernel` lists each kernel of the surface at its BASELINE config, timed alone: after 25
+untimed repetitions, each of 100 repetitions flushes the caches and times one burst of
+launches between one pair of events (memory-bound kernels: one launch per distinct buffer
+set, ~1 GiB touched in all, so every launch reads HBM; compute-bound kernels: 5 launches of
+the same operands); `achieved` comes from the median. Memory-bound entries carry the
+fraction of their mix ceiling, and each entry of configs[0], [1], [2]/[3] and [4] the
+oracle's time for the full config (`cpu`: one thread and all cores, sampled and scaled where
+the sample says so). `ceilings` lists the hk_hbm_stream rates themselves.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--suite headline|all]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+                       [--suite headline|all|kernels|compute|ceiling|copy] [--cases a,b]
 """
 from __future__ import annotations
 
@@ -34,16 +41,22 @@ def _args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--suite", choices=["headline", "all", "copy", "compute"], default="all",
+    ap.add_argument("--suite", choices=["headline", "all", "copy", "compute", "kernels",
+                                        "ceiling"],
+                    default="all",
                     help="copy: only the plain-copy kernel used to calibrate rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE counters (prints its byte count); compute: "
                          "only the MFMA kernels (GEMMs, attention) of the per-kernel suite, for "
-                         "counter runs")
+                         "counter runs; kernels: only the per-kernel suite; ceiling: only the "
+                         "HBM read/write-mix streams that bound the memory-bound kernels")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cases", default="",
-                    help="with --suite compute: comma-separated names of the cases to run "
-                         "(default: all)")
-    ap.add_argument("--reps", type=int, default=20, help="repetitions per per-kernel timing")
+                    help="with --suite compute or kernels: comma-separated names of the "
+                         "per-kernel cases to run (default: all)")
+    ap.add_argument("--reps", type=int, default=100,
+                    help="timed repetitions per per-kernel timing (the median is reported)")
+    ap.add_argument("--warmup-reps", type=int, default=25,
+                    help="untimed repetitions before each per-kernel timing")
     return ap.parse_args()
 
 
@@ -81,39 +94,29 @@ class Flusher:
         self.buf.sum()  # one reduction kernel over the fp32 buffer: reads only
 
 
-def time_kernel(fn, reps, flush=None):
-    """Average duration (ms) of fn's launches, each bracketed by events on the current stream."""
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-    fn()
-    torch.cuda.synchronize()
-    for i in range(reps):
-        if flush:
-            flush()
-        starts[i].record()
-        fn()
-        ends[i].record()
-    torch.cuda.synchronize()
-    ts = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
-    return {"avg_ms": sum(ts) / len(ts), "median_ms": ts[len(ts) // 2], "min_ms": ts[0]}
-
-
-def time_burst(fns, reps, flush):
-    """Average duration (ms) of one launch in a burst: each repetition flushes the caches, then
+def time_burst(fns, reps, flush, warmup=0):
+    """Duration (ms) of one launch in a burst: each repetition flushes the caches, then
     launches every fn of `fns` back to back between one pair of events on the current stream
     and divides by len(fns). For memory-bound kernels `fns` run on distinct buffer sets (each
     set is read from HBM once per burst), for compute-bound ones they repeat one launch.
-    One event pair per burst keeps the ~5 us event overhead out of short kernels."""
-    for f in fns:
-        f()
+    One event pair per burst keeps the ~5 us event overhead out of short kernels (the host
+    enqueues faster than these kernels run: the same bursts replayed from a HIP graph measured
+    2-4% slower, not faster). `warmup` untimed repetitions come first; mean, median and
+    minimum of the `reps` timed ones are returned (the reference reports the median of 100
+    runs after 25 warm-ups with the L2 flushed, README.md:137-139)."""
+    def body():
+        for f in fns:
+            f()
+    for _ in range(max(1, warmup)):
+        flush()
+        body()
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
     for i in range(reps):
         flush()
         starts[i].record()
-        for f in fns:
-            f()
+        body()
         ends[i].record()
     torch.cuda.synchronize()
     ts = sorted(s.elapsed_time(e) / len(fns) for s, e in zip(starts, ends))
@@ -194,19 +197,45 @@ def run_headline():
 
 
 # ------------------------------------------------------------------------------------------------
-# CPU baseline: the oracle on a bounded sample of the step
+# CPU baseline: the oracle on bounded samples, on one thread and on every core the host gives
 # ------------------------------------------------------------------------------------------------
-def run_cpu_baseline():
-    """Full configs[1] steps through the oracle on this host's cores, repeated until about 10 s
-    of CPU work is timed (a step takes ~1.2 s on 8 threads).
-
-    Inputs come from numpy's generator (untimed); the timed region is the five oracle calls
-    at the full GPU shapes, so the figure is directly comparable with the headline value."""
+def cpu_threads():
+    """(threads for the all-core leg, host facts). The all-core leg uses every core of this
+    process's affinity mask, or OMP_NUM_THREADS when the host sets it (the GPU boxes set it to
+    the process's CPU share, which can be fewer than the machine's cores)."""
     import oracle
 
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    cores = max(1, min(cores, 16))
-    oracle.set_threads(cores)
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    env = os.environ.get("OMP_NUM_THREADS")
+    threads = int(env) if env and env.isdigit() and int(env) > 0 else affinity
+    facts = {"hardware_concurrency": oracle.hardware_concurrency(), "affinity_cores": affinity,
+             "omp_num_threads_env": env}
+    return max(1, threads), facts
+
+
+def _cpu_time(fn, min_s=0.2):
+    """Mean seconds per call of fn: one untimed call, then calls until min_s has elapsed."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s:
+            return dt / n
+
+
+def run_cpu_baseline():
+    """configs[1] steps through the oracle: all cores on the full step, repeated until ~10 s of
+    CPU work is timed; one thread on a quarter of the step (a quarter of the GELU elements, CE
+    rows and AdamW parameters; every element is independent), scaled by 4.
+
+    Inputs come from numpy's generator (untimed); the timed region is the five oracle calls,
+    so the figure is directly comparable with the headline value. Returns the cpu_baseline
+    object and each step kernel's CPU time (ms, full size)."""
+    import oracle
+
+    threads, facts = cpu_threads()
     rng = np.random.default_rng(7)
     n = 8 * 1024 * 3072
     x = oracle.f32_to_bf16(rng.standard_normal(n, dtype=np.float32))
@@ -222,25 +251,148 @@ def run_cpu_baseline():
     v = rng.random(P, dtype=np.float32) * np.float32(0.1)
     grad = np.zeros_like(logits)  # output pages touched before the timed region
     c = W.ADAMW
-    reps, dt = 0, 0.0
-    while dt < 10.0 and reps < 50:  # repeat the full step until ~10 s of CPU work is timed
+    names = ["gelu_fwd_bf16", "ce_fwd", "ce_bwd", "gelu_bwd_bf16", "adamw_148"]
+
+    def step(frac):
+        ne, nr, npar = n // frac, rows // frac, P // frac
+        t = []
         t0 = time.perf_counter()
-        y = oracle.gelu_forward(x)
-        loss, mx, sm = oracle.sparse_ce_forward(logits, targets)
-        gr = oracle.sparse_ce_backward(logits, targets, mx, sm, 1.0, out=grad)
-        gi = oracle.gelu_backward(dy, x)
-        oracle.adamw_(p, g, m, v, c["lr"], c["beta1"], c["beta2"], c["eps"], c["weight_decay"],
-                      1 - c["beta1"], 1 - c["beta2"])
-        dt += time.perf_counter() - t0
+        oracle.gelu_forward(x[:ne])
+        t.append(time.perf_counter())
+        _, mx, sm = oracle.sparse_ce_forward(logits[:nr], targets[:nr])
+        t.append(time.perf_counter())
+        oracle.sparse_ce_backward(logits[:nr], targets[:nr], mx, sm, 1.0, out=grad[:nr])
+        t.append(time.perf_counter())
+        oracle.gelu_backward(dy[:ne], x[:ne])
+        t.append(time.perf_counter())
+        oracle.adamw_(p[:npar], g[:npar], m[:npar], v[:npar], c["lr"], c["beta1"], c["beta2"],
+                      c["eps"], c["weight_decay"], 1 - c["beta1"], 1 - c["beta2"])
+        t.append(time.perf_counter())
+        return [b - a for a, b in zip([t0] + t[:-1], t)]
+
+    oracle.set_threads(threads)
+    reps, per = 0, [0.0] * 5
+    while sum(per) < 10.0 and reps < 50:  # repeat the full step until ~10 s of CPU work is timed
+        per = [a + b for a, b in zip(per, step(1))]
         reps += 1
-    del y, gr, gi, logits, grad
+    dt = sum(per)
+    oracle.set_threads(1)
+    per1 = [4 * t for t in step(4)]  # a quarter of the step, scaled to the full step
+    oracle.set_threads(threads)
+    del logits, grad
     nbytes = (W.gelu_fwd_bytes(n, 2) + W.gelu_bwd_bytes(n, 2) + W.ce_fwd_bytes(rows, V)
               + W.ce_bwd_bytes(rows, V) + W.adamw_bytes(P))
-    return {"value": round(reps * nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": cores,
+    base = {"value": round(reps * nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": (f"{reps} full configs[1] steps (GELU fwd+bwd bf16 {n} elements, CE fwd+bwd "
                        f"{rows}x{V}, AdamW {P} params) through the oracle, the C++ restatement of "
-                       f"the reference harnesses' CPU references; {dt:.2f} s on {cores} threads")}
+                       f"the reference harnesses' CPU references; {dt:.2f} s on {threads} threads"),
+            "value_1thread": round(nbytes / sum(per1) / 1e9, 3),
+            "sample_1thread": ("a quarter of one configs[1] step (1/4 of the GELU elements, CE "
+                               "rows and AdamW parameters) on 1 thread, scaled by 4: "
+                               f"{sum(per1) / 4:.2f} s"),
+            **facts}
+    kernels = {k: {"ms_all_cores": round(a / reps * 1e3, 3), "ms_1thread": round(b * 1e3, 3),
+                   "threads": threads, "sample": "configs[1] step (see cpu_baseline)"}
+               for k, a, b in zip(names, per, per1)}
+    return base, kernels
+
+
+def run_cpu_configs():
+    """The oracle at configs[0], [2]/[3] and [4] (and the reduce at the README shape), on one
+    thread and on every core, each figure scaled to the full config (ms). Large configs are
+    sampled: attention runs whole heads (1 on one thread, one per thread on all cores) and is
+    scaled to the 96 heads of the config; the GEMMs and the reduce run whole output rows and are
+    scaled to the config's rows. Every sampled unit is independent work of the same size."""
+    import oracle
+
+    threads, _ = cpu_threads()
+    rng = np.random.default_rng(11)
+    out = {}
+
+    def both(name, make, full_units, units_per_thread, unit):
+        """make(units) -> fn timing `units` units; scaled by full_units / units."""
+        entry = {"threads": threads}
+        for leg, th in (("ms_1thread", 1), ("ms_all_cores", threads)):
+            oracle.set_threads(th)
+            u = min(full_units, units_per_thread * th)
+            entry[leg] = round(_cpu_time(make(u)) * full_units / u * 1e3, 3)
+            entry["sample_" + leg[3:]] = (f"{u} of {full_units} {unit}"
+                                          + (f", scaled by {full_units / u:g}" if u < full_units
+                                             else ""))
+        out[name] = entry
+        log("cpu", name, entry)
+
+    # configs[0]: LayerNorm fp32 4096 x 768, whole
+    R, C = W.LN["rows"], W.LN["cols"]
+    x = rng.standard_normal((R, C), dtype=np.float32)
+    dyl = rng.standard_normal((R, C), dtype=np.float32)
+    gam = (rng.random(C, dtype=np.float32) + np.float32(0.5))
+    bet = rng.standard_normal(C, dtype=np.float32) * np.float32(0.1)
+    _, mu, rs = oracle.layer_norm_forward(x, gam, bet, W.LN["eps"])
+    both("ln_fwd", lambda u: lambda: oracle.layer_norm_forward(x[:u], gam, bet, W.LN["eps"]),
+         R, R, "rows")
+    both("ln_bwd_input", lambda u: lambda: oracle.ln_backward_input(dyl[:u], x[:u], mu[:u],
+                                                                   rs[:u], gam), R, R, "rows")
+    both("ln_bwd_gamma_beta", lambda u: lambda: oracle.ln_backward_gamma_beta(dyl[:u], x[:u],
+                                                                           mu[:u], rs[:u]),
+         R, R, "rows")
+    fused = {}
+    for leg in ("ms_1thread", "ms_all_cores"):  # the oracle has no fused form: the two summed
+        fused[leg] = round(out["ln_bwd_input"][leg] + out["ln_bwd_gamma_beta"][leg], 3)
+        fused["sample_" + leg[3:]] = "ln_bwd_input + ln_bwd_gamma_beta"
+    out["ln_bwd_fused"] = {"threads": threads, **fused}
+    # configs[2] / [3]: attention B=8 H=12 T=1024 d=64
+    A = W.ATTN
+    heads, T, D = A["B"] * A["H"], A["T"], A["d"]
+    nh = min(heads, threads)
+    q, k, v, do = (rng.standard_normal((1, nh, T, D), dtype=np.float32) for _ in range(4))
+    scale = D ** -0.5
+    for causal in (False, True):
+        tag = "causal" if causal else "noncausal"
+        o, lse = oracle.attn_forward(q, k, v, scale, causal)
+        shape = f"{A['B']}x{A['H']}x{T}x{D}"
+        both(f"attn_fwd_{tag}_{shape}", lambda u, causal=causal: lambda: oracle.attn_forward(
+            q[:, :u], k[:, :u], v[:, :u], scale, causal), heads, 1, "(b, h) heads")
+        both(f"attn_bwd_{tag}_{shape}", lambda u, causal=causal, o=o, lse=lse: lambda: oracle.attn_backward(
+            q[:, :u], k[:, :u], v[:, :u], o[:, :u], do[:, :u], lse[:, :u], scale, causal),
+            heads, 1, "(b, h) heads")
+    # configs[4]: BF16 GEMM 8192 x 5120 x 1280 in four layouts, its dA / dB, SGEMM 4096^3 + bias
+    G = W.BGEMM
+    M, N, K = G["M"], G["N"], G["K"]
+    bf = lambda *shape: oracle.f32_to_bf16(  # noqa: E731
+        rng.standard_normal(shape, dtype=np.float32) * np.float32(0.05))
+    rows_pt = 16
+    a_mk, b_kn = bf(rows_pt * threads, K), bf(K, N)
+    a_km, b_nk = np.ascontiguousarray(a_mk.T), np.ascontiguousarray(b_kn.T)
+    for ta, tb in ((0, 0), (0, 1), (1, 0), (1, 1)):
+        bb = b_nk if tb else b_kn
+        name = f"bgemm_{'T' if ta else 'N'}{'T' if tb else 'N'}_8192x5120x1280"
+        both(name, lambda u, ta=ta, tb=tb, bb=bb: lambda: oracle.bgemm(
+            ta, tb, np.ascontiguousarray(a_km[:, :u]) if ta else a_mk[:u], bb), M, rows_pt,
+            "output rows")
+    # dA = dY W^T: [M, N] x [K, N]^T; dB = X^T dY: [M, K]^T x [M, N] (M rows of the product are K)
+    dy_mn, w_kn = bf(rows_pt * threads, N), bf(K, N)
+    both("bgemm_dA_NT_8192x1280x5120", lambda u: lambda: oracle.bgemm(0, 1, dy_mn[:u], w_kn), M,
+         rows_pt, "output rows")
+    x_mk, dy_full = bf(M, 4 * threads), bf(M, N)
+    both("bgemm_dB_TN_1280x5120x8192", lambda u: lambda: oracle.bgemm(
+        1, 0, np.ascontiguousarray(x_mk[:, :u]), dy_full), K, 4, "output rows")
+    S = W.SGEMM
+    sa = rng.standard_normal((4 * threads, S["K"]), dtype=np.float32)
+    sb = rng.standard_normal((S["K"], S["N"]), dtype=np.float32)
+    sbias = rng.standard_normal(S["N"], dtype=np.float32)
+    # one CPU figure serves both GPU lines (the split is a GPU scheduling choice)
+    both("sgemm_NN_4096^3_splitk4_bias", lambda u: lambda: oracle.sgemm(0, 0, sa[:u], sb,
+                                                                       bias=sbias), S["M"], 4,
+         "output rows")
+    out["sgemm_NN_4096^3_auto_split_bias"] = out["sgemm_NN_4096^3_splitk4_bias"]
+    # unified reduce, README shape 16384 x 50304 (inner axis)
+    rsrc = rng.standard_normal((1024 * threads, 50304), dtype=np.float32)
+    both("reduce_inner_16384x50304", lambda u: lambda: oracle.reduce_inner(rsrc[:u], u, 50304),
+         16384, 1024, "output rows")
+    oracle.set_threads(threads)
+    return out
 
 
 # ------------------------------------------------------------------------------------------------
@@ -251,14 +403,7 @@ def per_kernel_suite(flush, compute_only=False):
     g = torch.Generator(device=DEV)
     g.manual_seed(99)
     if compute_only:
-        cases = gemm_cases(g) + attention_cases(g)
-        if ARGS.cases:
-            keep = set(ARGS.cases.split(","))
-            unknown = keep - {c[0] for c in cases}
-            if unknown:
-                raise SystemExit(f"bench.py: unknown case(s) {sorted(unknown)}")
-            cases = [c for c in cases if c[0] in keep]
-        return time_cases(cases, flush, out)
+        return time_cases(select(gemm_cases(g) + attention_cases(g)), flush, out)
     # LayerNorm configs[0], in fp32 and in bf16 / fp16 storage (fp32 statistics); gamma and
     # beta are shared by the buffer sets
     R, C = W.LN["rows"], W.LN["cols"]
@@ -270,7 +415,7 @@ def per_kernel_suite(flush, compute_only=False):
         g16, b16 = gamma.to(dt), beta.to(dt)
         dgam = torch.zeros(C, device=DEV)
         dbet = torch.zeros(C, device=DEV)
-        fwd, bwd = [], []
+        fwd, bwd, bin_, bgb = [], [], [], []
         for _ in range(n_sets(W.ln_bwd_bytes(R, C, es))):
             x = torch.randn(R, C, generator=g, device=DEV).to(dt)
             dy = torch.randn(R, C, generator=g, device=DEV).to(dt)
@@ -282,8 +427,15 @@ def per_kernel_suite(flush, compute_only=False):
                        hk.layer_norm_forward(x, g16, b16, W.LN["eps"], y, mean, rstd))
             bwd.append(lambda dy=dy, x=x, mean=mean, rstd=rstd, dx=dx, g16=g16, dgam=dgam,
                        dbet=dbet: hk.layer_norm_backward(dy, x, mean, rstd, g16, dgam, dbet, dx))
+            bin_.append(lambda dy=dy, x=x, mean=mean, rstd=rstd, dx=dx, g16=g16:
+                        hk.ln_backward_input(dy, x, mean, rstd, g16, dx))
+            bgb.append(lambda dy=dy, x=x, mean=mean, rstd=rstd, dgam=dgam, dbet=dbet:
+                       hk.ln_backward_gamma_beta(dy, x, mean, rstd, dgam, dbet))
         cases += [(f"ln_fwd{tag}", fwd, W.ln_fwd_bytes(R, C, es), "hbm"),
                   (f"ln_bwd_fused{tag}", bwd, W.ln_bwd_bytes(R, C, es), "hbm")]
+        if not tag:  # the two separate backward entry points, fp32
+            cases += [("ln_bwd_input", bin_, W.ln_bwd_bytes(R, C, es), "hbm"),
+                      ("ln_bwd_gamma_beta", bgb, W.ln_fwd_bytes(R, C, es), "hbm")]
     # GELU in fp16 at the configs[1] shape (the headline step runs the bf16 form)
     n = W.numel(W.GELU["shape"])
     gf, gb = [], []
@@ -306,28 +458,40 @@ def per_kernel_suite(flush, compute_only=False):
     cases += gemm_cases(g)
     cases += gemv_cases(g)
     cases += attention_cases(g)
-    return time_cases(cases, flush, out)
+    return time_cases(select(cases), flush, out)
+
+
+def select(cases):
+    """The cases --cases names (all when it is empty)."""
+    if not ARGS.cases:
+        return cases
+    keep = set(ARGS.cases.split(","))
+    unknown = keep - {c[0] for c in cases}
+    if unknown:
+        raise SystemExit(f"bench.py: unknown case(s) {sorted(unknown)}")
+    return [c for c in cases if c[0] in keep]
 
 
 def time_cases(cases, flush, out):
-    """Times each (name, fn or [fns], work, bound) case; fills and returns `out`."""
+    """Times each (name, fn or [fns], work, bound) case; fills and returns `out`. `achieved` and
+    `frac` come from the median burst (the reference's statistic); the mean is listed beside."""
     for name, fn, work, bound in cases:
         fns = fn if isinstance(fn, list) else [fn] * (1 if bound == "hbm" else COMPUTE_BURST)
-        t = time_burst(fns, ARGS.reps, flush)
+        t = time_burst(fns, ARGS.reps, flush, ARGS.warmup_reps)
+        ms = t["median_ms"]
+        entry = {"median_ms": round(ms, 5), "avg_ms": round(t["avg_ms"], 5),
+                 "reps": ARGS.reps, "warmup_reps": ARGS.warmup_reps}
         if bound == "hbm":
-            ach = work / (t["avg_ms"] * 1e-3) / 1e9
-            out[name] = {"avg_ms": round(t["avg_ms"], 5), "achieved": round(ach, 1), "unit": "GB/s",
-                         "frac": round(ach / W.PEAK_HBM_GBS, 4)}
+            ach = work / (ms * 1e-3) / 1e9
+            entry.update({"achieved": round(ach, 1), "unit": "GB/s",
+                          "frac": round(ach / W.PEAK_HBM_GBS, 4)})
         else:
-            ach = work / (t["avg_ms"] * 1e-3) / 1e12
+            ach = work / (ms * 1e-3) / 1e12
             peak = W.PEAK_TFLOPS[bound]
-            out[name] = {"avg_ms": round(t["avg_ms"], 5), "achieved": round(ach, 1),
-                         "unit": "TFLOP/s", "peak": peak, "frac": round(ach / peak, 4)}
-            if bound == "bf16x3":
-                # the same fp32-I/O work priced against the fp32 MFMA peak (the other choice the
-                # north star allows): above 1 means faster than any fp32-MFMA kernel can be
-                out[name]["frac_of_fp32_mfma_peak"] = round(ach / W.PEAK_TFLOPS["fp32_matrix"], 4)
-        log(name, out[name])
+            entry.update({"achieved": round(ach, 1), "unit": "TFLOP/s", "peak": peak,
+                          "frac": round(ach / peak, 4)})
+        out[name] = entry
+        log(name, entry)
     return out
 
 
@@ -484,6 +648,90 @@ TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profile
                             "traffic_configs1_step.txt")
 
 
+# ------------------------------------------------------------------------------------------------
+# HBM read/write-mix ceilings
+# ------------------------------------------------------------------------------------------------
+# (name, fp32 elements per array, arrays read, arrays written): each memory-bound kernel of the
+# surface at its own mix and byte count, plus 1 GiB-per-array read, write and copy streams.
+CEILINGS = [
+    ("ceiling_1r1w_ln_fp32", 4096 * 768, 1, 1),         # LayerNorm forward fp32, configs[0]
+    ("ceiling_2r1w_ln_fp32", 4096 * 768, 2, 1),         # LayerNorm backward fp32
+    ("ceiling_1r1w_ln_16bit", 4096 * 768 // 2, 1, 1),   # LayerNorm forward bf16 / fp16
+    ("ceiling_2r1w_ln_16bit", 4096 * 768 // 2, 2, 1),   # LayerNorm backward bf16 / fp16
+    ("ceiling_1r1w_gelu_16bit", 8 * 1024 * 3072 // 2, 1, 1),  # GELU forward, configs[1]
+    ("ceiling_2r1w_gelu_16bit", 8 * 1024 * 3072 // 2, 2, 1),  # GELU backward
+    ("ceiling_1r0w_ce", 8192 * 50257, 1, 0),            # CE forward reads the logits
+    ("ceiling_1r1w_ce", 8192 * 50257, 1, 1),            # CE backward: logits in, grad out
+    ("ceiling_4r3w_adamw", 124_439_808, 4, 3),          # AdamW: p, g, m, v in; p, m, v out
+    ("ceiling_1r0w_1GiB", 1 << 28, 1, 0),
+    ("ceiling_0r1w_1GiB", 1 << 28, 0, 1),
+    ("ceiling_1r1w_1GiB", 1 << 28, 1, 1),
+]
+# memory-bound per-kernel case -> the ceiling of its mix and size
+CEILING_OF = {
+    "ln_fwd": "ceiling_1r1w_ln_fp32", "ln_bwd_fused": "ceiling_2r1w_ln_fp32",
+    "ln_bwd_input": "ceiling_2r1w_ln_fp32",
+    "ln_fwd_bf16": "ceiling_1r1w_ln_16bit", "ln_bwd_fused_bf16": "ceiling_2r1w_ln_16bit",
+    "ln_fwd_f16": "ceiling_1r1w_ln_16bit", "ln_bwd_fused_f16": "ceiling_2r1w_ln_16bit",
+    "gelu_fwd_bf16": "ceiling_1r1w_gelu_16bit", "gelu_bwd_bf16": "ceiling_2r1w_gelu_16bit",
+    "gelu_fwd_f16": "ceiling_1r1w_gelu_16bit", "gelu_bwd_f16": "ceiling_2r1w_gelu_16bit",
+    "ce_fwd": "ceiling_1r0w_ce", "ce_bwd": "ceiling_1r1w_ce", "adamw_148": "ceiling_4r3w_adamw",
+    "reduce_inner_16384x50304": "ceiling_1r0w_1GiB",
+}
+
+
+def ceiling_suite(flush, names=None):
+    """Times hk_hbm_stream at each CEILINGS mix (the best of 1, 2 and 4 spans per workgroup),
+    each burst over distinct buffer sets as for the memory-bound kernels."""
+    import ctypes
+
+    lib = hk.lib()
+    out = {}
+    for name, n, nin, nout in CEILINGS:
+        if names is not None and name not in names:
+            continue
+        nbytes = 4 * n * (nin + nout)
+        sets = []
+        for _ in range(n_sets(nbytes)):
+            ins = [torch.randn(n, device=DEV) for _ in range(nin)]
+            outs = [torch.empty(n, device=DEV) for _ in range(nout)]
+            sets.append((ins, outs))
+        sink = torch.empty(-(-n // 1024), device=DEV)
+        best = None
+        for unroll in (1, 2, 4):
+            fns = []
+            for ins, outs in sets:
+                pin = (ctypes.c_void_p * 4)(*[t.data_ptr() for t in ins])
+                pout = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in outs])
+
+                def run(pin=pin, pout=pout, unroll=unroll):
+                    st = lib.hk_hbm_stream(pin, nin, pout, nout, n, unroll, sink.data_ptr(),
+                                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+                    assert st == 0
+                fns.append(run)
+            t = time_burst(fns, ARGS.reps, flush, ARGS.warmup_reps)
+            if best is None or t["median_ms"] < best[1]["median_ms"]:
+                best = (unroll, t)
+        unroll, t = best
+        ach = nbytes / (t["median_ms"] * 1e-3) / 1e9
+        out[name] = {"median_ms": round(t["median_ms"], 5), "avg_ms": round(t["avg_ms"], 5),
+                     "achieved": round(ach, 1), "unit": "GB/s",
+                     "frac": round(ach / W.PEAK_HBM_GBS, 4), "bytes": nbytes,
+                     "reads": nin, "writes": nout, "spans_per_workgroup": unroll}
+        log(name, out[name])
+        del sets, sink
+    return out
+
+
+def attach_ceilings(per_kernel, ceilings):
+    """Adds the measured mix ceiling and the fraction of it to every memory-bound entry."""
+    for k, c in CEILING_OF.items():
+        if k in per_kernel and c in ceilings and per_kernel[k].get("unit") == "GB/s":
+            per_kernel[k]["mix_ceiling"] = c
+            per_kernel[k]["frac_of_mix_ceiling"] = round(
+                per_kernel[k]["achieved"] / ceilings[c]["achieved"], 4)
+
+
 def run_copy_calibration():
     """A plain copy of known size (1 GiB read, 1 GiB written) for counter calibration."""
     src = torch.randn(COPY_BYTES // 4, device=DEV)
@@ -502,6 +750,12 @@ def main():
     if ARGS.suite == "compute":
         print(json.dumps({"per_kernel": per_kernel_suite(Flusher(), compute_only=True)}),
               flush=True)
+        return
+    if ARGS.suite == "kernels":
+        print(json.dumps({"per_kernel": per_kernel_suite(Flusher())}), flush=True)
+        return
+    if ARGS.suite == "ceiling":
+        print(json.dumps({"ceilings": ceiling_suite(Flusher())}), flush=True)
         return
     ks, step_bytes, ms_step, per = run_headline()
     value = step_bytes / (ms_step * 1e-3) / 1e9
@@ -533,13 +787,30 @@ def main():
                      "peak": W.PEAK_HBM_GBS, "unit": "GB/s", "frac": round(ach / W.PEAK_HBM_GBS, 4),
                      "traffic": traffic.get(dom), "algorithmic_bytes": byte_of[dom]},
     }
+    flush = Flusher()
+    # the HBM rate the dominant kernel's read/write mix reaches at its size (hk_hbm_stream)
+    ceilings = ceiling_suite(flush, None if ARGS.suite == "all" else {CEILING_OF[dom]})
+    c = ceilings[CEILING_OF[dom]]
+    result["roofline"]["mix_ceiling"] = {"stream": CEILING_OF[dom], "achieved": c["achieved"],
+                                         "frac_of_mix_ceiling": round(ach / c["achieved"], 4)}
     if ARGS.suite == "all":
         result["per_kernel"] = {n: {"avg_ms": round(per[n], 5),
                                     "achieved": round(byte_of[n] / (per[n] * 1e-3) / 1e9, 1),
-                                    "unit": "GB/s"} for n in per}
-        result["per_kernel"].update(per_kernel_suite(Flusher()))
+                                    "unit": "GB/s",
+                                    "frac": round(byte_of[n] / (per[n] * 1e-3) / 1e9
+                                                  / W.PEAK_HBM_GBS, 4),
+                                    "timing": "inside the step, mean of steps"}
+                                for n in per}
+        result["per_kernel"].update(per_kernel_suite(flush))
+        attach_ceilings(result["per_kernel"], ceilings)
+        result["ceilings"] = ceilings
     if not ARGS.no_cpu:
-        result["cpu_baseline"] = run_cpu_baseline()
+        result["cpu_baseline"], cpu_kernels = run_cpu_baseline()
+        if ARGS.suite == "all":
+            cpu_kernels.update(run_cpu_configs())
+            for k, e in cpu_kernels.items():
+                if k in result["per_kernel"]:
+                    result["per_kernel"][k]["cpu"] = e
     print(json.dumps(result), flush=True)
 
 
