@@ -10,9 +10,14 @@
 // group w % 4 (32 keys) and query half w / 4 of every 64-query tile, so each SIMD runs two
 // waves. gfx950 has no TF32 MFMA; every product runs as a bf16x3 split on
 // v_mfma_f32_32x32x16_bf16 (x = hi + lo in bf16, a b = ah bh + ah bl + al bh accumulated in
-// fp32, relative error ~1e-5). K and V of the tile are split and staged into LDS once; query
-// tiles (Q, dO, LSE, D) are split and stream through LDS with the next tile's global loads in
-// flight. All LDS operands are bf16 hi / lo pairs of [rows][64] arrays (128-byte rows) read two
+// fp32, relative error ~1e-5). K and V of the tile are split and staged into LDS once. Q and dO
+// are split once per call by a pre-pass into bf16 hi / lo planes ([b, h][T][64], plus LSE log2(e)
+// and D as contiguous [b, h][T] rows), and each query tile is copied from them straight into LDS
+// (global_load_lds, no registers): the copies of tile i + 1 are issued once every wave is done
+// reading tile i's Q / dO and land during tile i's dQ phase. Splitting in every key-tile
+// workgroup instead (8 x per query row at T = 1024) cost 14% of the kernel in VALU and LDS
+// stores, and holding the next tile's fp32 rows in registers another 15% at the BASELINE shape.
+// All LDS operands are bf16 hi / lo pairs of [rows][64] arrays (128-byte rows) read two
 // ways: 16-byte reads for a contraction over the head dimension, and the gfx950 transposing read
 // ds_read_b64_tr_b16 for a contraction over rows, so each tensor is stored once. Per query tile
 // a wave forms S = Q K^T and dP = dO V^T for its 32 x 32 block (accumulators hold one key column
@@ -143,17 +148,80 @@ struct Stager {
   }
 };
 
-__global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_params p, int nbh) {
+// 16-byte (4-byte) global -> LDS copy of one lane (global_load_lds_dwordx4 / _dword): the wave's
+// 64 lanes write 1 KiB (256 bytes) of LDS at m0 + 16 (4) * lane. Address = sbase (wave-uniform,
+// SGPRs) + voff (per-lane byte offset). Inline asm, so the compiler does not wait for every copy
+// before each LDS read; the kernel waits for the copies itself (vmcnt) before the barrier that
+// publishes a tile. m0 is an input operand, so the compiler knows the asm sets it.
+// The compiler's hazard checks do not see inside the asm: when sbase was just reloaded from a
+// spill slot (v_readlane, a VALU write of the SGPRs), the VMEM read of it needs 5 wait states,
+// which the leading s_nop 4 provides (without it the copy can use a stale address).
+__device__ __forceinline__ void copy16_to_lds(const void* sbase, int voff, unsigned lds_addr) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+               "{m0}"(lds_addr));
+}
+__device__ __forceinline__ void copy4_to_lds(const void* sbase, int voff, unsigned lds_addr) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase),
+               "{m0}"(lds_addr));
+}
+
+// Pre-split query-side operands of one call: bf16 hi / lo planes of Q and dO, [b, h][T][64]
+// (128-byte rows), and LSE * log2(e) and D as [b, h][T].
+struct QPlanes {
+  const char* qh;
+  const char* ql;
+  const char* oh;
+  const char* ol;
+  const float* l2;
+  const float* d;
+};
+
+// Vector memory operations each lane issues after a tile's copies: the dQ atomics. A wave
+// waits with vmcnt(kAtomicsPerTile) for its copies of the next tile (vector memory operations
+// complete in issue order), so the atomics themselves are never waited for.
+constexpr int kAtomicsPerTile = 8;
+
+// The pre-pass: grid (ceil(T * 8 / 256), B * nh); thread t of the row-chunk index covers 8
+// consecutive d of one row of Q and of dO.
+__global__ __launch_bounds__(256) void attn_bwd_prepare(hk_attn_bwd_params p, char* qh, char* ql,
+                                                        char* oh, char* ol, float* l2, float* dd) {
+  const int bh = blockIdx.y;
+  const int b = bh / p.nh, h = bh - b * p.nh;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t row = idx >> 3;
+  const int chunk = static_cast<int>(idx & 7);
+  if (row >= p.T) return;
+  const float* q = p.Q + b * p.q_strideB + h * p.q_strideH + row * p.q_strideM + 8 * chunk;
+  const float* o = p.dO + b * p.do_strideB + h * p.do_strideH + row * p.do_strideM + 8 * chunk;
+  const int64_t dst = ((static_cast<int64_t>(bh) * p.T + row) * 8 + chunk) * 16;
+  const f32x4_t q0 = *reinterpret_cast<const f32x4_t*>(q);
+  const f32x4_t q1 = *reinterpret_cast<const f32x4_t*>(q + 4);
+  const f32x4_t o0 = *reinterpret_cast<const f32x4_t*>(o);
+  const f32x4_t o1 = *reinterpret_cast<const f32x4_t*>(o + 4);
+  const float xq[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+  const float xo[8] = {o0[0], o0[1], o0[2], o0[3], o1[0], o1[1], o1[2], o1[3]};
+  u32x4_t hi, lo;
+  split8(xq, hi, lo);
+  *reinterpret_cast<u32x4_t*>(qh + dst) = hi;
+  *reinterpret_cast<u32x4_t*>(ql + dst) = lo;
+  split8(xo, hi, lo);
+  *reinterpret_cast<u32x4_t*>(oh + dst) = hi;
+  *reinterpret_cast<u32x4_t*>(ol + dst) = lo;
+  if (chunk == 0) {
+    const int64_t r = static_cast<int64_t>(bh) * p.T + row;
+    l2[r] = p.LSE[b * p.lse_strideB + h * p.lse_strideH + row] * kLog2e;
+    dd[r] = p.D[b * p.d_strideB + h * p.d_strideH + row];
+  }
+}
+
+__global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_params p, int nbh,
+                                                                QPlanes qp) {
   extern __shared__ __attribute__((aligned(16))) char lds_generic[];
   char HK_LDS* lds = (char HK_LDS*)lds_generic;
   char HK_LDS* sKh = lds + kOffKh;
   char HK_LDS* sKl = lds + kOffKl;
   char HK_LDS* sVh = lds + kOffVh;
   char HK_LDS* sVl = lds + kOffVl;
-  char HK_LDS* sQh = lds + kOffQh;
-  char HK_LDS* sQl = lds + kOffQl;
-  char HK_LDS* sOh = lds + kOffOh;
-  char HK_LDS* sOl = lds + kOffOl;
   char HK_LDS* sSh = lds + kOffSh;
   char HK_LDS* sSl = lds + kOffSl;
   float HK_LDS* sL = (float HK_LDS*)(lds + kOffL);
@@ -168,15 +236,11 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
   const int b = bh / p.nh, h = bh - b * p.nh;
   const int64_t k0 = static_cast<int64_t>(kt) * kBKV;
 
-  const float* Qb = p.Q + b * p.q_strideB + h * p.q_strideH;
   const float* Kb = p.K + b * p.k_strideB + h * p.k_strideH;
   const float* Vb = p.V + b * p.v_strideB + h * p.v_strideH;
-  const float* dOb = p.dO + b * p.do_strideB + h * p.do_strideH;
-  const float* Lb = p.LSE + b * p.lse_strideB + h * p.lse_strideH;
-  const float* Db = p.D + b * p.d_strideB + h * p.d_strideH;
   float* dQb = p.dQ + b * p.dq_strideB + h * p.dq_strideH;
 
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int c = lane & 31;
   const int hh = lane >> 5;
@@ -196,18 +260,31 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
   const int64_t q_first = p.is_causal ? (k0 / kBQ) * kBQ : 0;
   const int nq = static_cast<int>((T - q_first + kBQ - 1) / kBQ);
 
-  Stager<kBQ> stq, sto;
-  float rl = 0.f, rd = 0.f;
-  auto fetch = [&](int64_t q0) {
-    stq.load(Qb, p.q_strideM, q0, T);
-    sto.load(dOb, p.do_strideM, q0, T);
-    if (threadIdx.x < kBQ) {
-      const int64_t qq = q0 + threadIdx.x;
-      rl = qq < T ? Lb[qq] * kLog2e : 0.f;
-      rd = qq < T ? Db[qq] : 0.f;
+  // Copies of query tile q0 into LDS: wave w moves rows 8 w .. 8 w + 7 of each of the four
+  // planes (lane l: row 8 w + l / 8, stored chunk l % 8, which holds logical chunk
+  // (l % 8) ^ swz(row)); waves 0 and 1 also move the 64 LSE * log2(e) and D values. Rows past
+  // T read row T - 1: they only meet masked keys / queries and are never stored.
+  const int64_t plane_row0 = static_cast<int64_t>(bh) * T;
+  const int crow = 8 * wave + (lane >> 3);
+  const int cchunk = (lane & 7) ^ swz(crow);
+  const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
+  auto copy_tile = [&](int64_t q0) {
+    const int64_t r = q0 + crow < T ? q0 + crow : T - 1;
+    const int voff = static_cast<int>(r * kRowBytes) + (cchunk << 4);
+    const int64_t head = plane_row0 * kRowBytes;
+    const unsigned dst = lds_base + 1024 * wave;
+    copy16_to_lds(qp.qh + head, voff, dst + kOffQh);
+    copy16_to_lds(qp.ql + head, voff, dst + kOffQl);
+    copy16_to_lds(qp.oh + head, voff, dst + kOffOh);
+    copy16_to_lds(qp.ol + head, voff, dst + kOffOl);
+    if (wave < 2) {
+      const int64_t rr = q0 + lane < T ? q0 + lane : T - 1;
+      copy4_to_lds((wave == 0 ? qp.l2 : qp.d) + plane_row0, static_cast<int>(rr * 4),
+                   lds_base + (wave == 0 ? kOffL : kOffD));
     }
   };
-  if (nq > 0) fetch(q_first);
+  if (nq > 0) copy_tile(q_first);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // dV, dK: C layout of (A = P^T or dS^T: rows = keys, B = dO or Q: columns = d):
   // key 32 kg + 8 (i/4) + 4 hh + i%4, d 32 db + c
@@ -261,15 +338,11 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
 
   for (int it = 0; it < nq; ++it) {
     const int64_t q0 = q_first + static_cast<int64_t>(it) * kBQ;
-    __syncthreads();  // previous tile's LDS reads (and the dQ exchange) are done
-    stq.store(sQh, sQl);
-    sto.store(sOh, sOl);
-    if (threadIdx.x < kBQ) {
-      sL[threadIdx.x] = rl;
-      sD[threadIdx.x] = rd;
-    }
+    // This tile's copies were issued before the previous tile's atomics: with those still in
+    // flight they are done once at most kAtomicsPerTile operations are outstanding. The barrier
+    // then publishes every wave's copies (and orders the previous tile's dQ exchange reads).
+    if (it > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAtomicsPerTile) : "memory");
     __syncthreads();
-    if (it + 1 < nq) fetch(q0 + kBQ);
 
     // This wave's block: keys k0 + 32 kg .. + 31, queries q0 + 32 qh .. + 31. Under causal
     // masking a block whose keys all follow its queries is zero; one whose keys all precede
@@ -300,8 +373,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
       // selects; edge blocks zero P where the query or key lies past T or the key follows the
       // query under causal masking (offsets relative to the block, 32-bit compares).
       auto p_ds = [&](auto masked) {
-        const int key_lim = static_cast<int>(min<int64_t>(T - kw, 32));  // keys kw + c < T
-        const int q_lim = static_cast<int>(min<int64_t>(T - qw, 32));    // queries qw + r < T
+        const int key_lim = T - kw < 32 ? static_cast<int>(T - kw) : 32;  // keys kw + c < T
+        const int q_lim = T - qw < 32 ? static_cast<int>(T - qw) : 32;    // queries qw + r < T
         const int cdiff = static_cast<int>(kw - qw);  // key - query = cdiff + c - r
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -379,6 +452,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
       }
     }
     __syncthreads();
+    // every wave is done with this tile's Q / dO / LSE / D: the next tile's copies land while
+    // the dQ phase runs
+    if (it + 1 < nq) copy_tile(q0 + kBQ);
     // dQ block (queries 32 qb.., d 32 dbq..), key half kh of this wave = dS[q][keys] K[keys][d]:
     // both operands are read transposed (contraction over their rows = keys).
     f32x16_t dq = f32x16_t{};
@@ -407,17 +483,22 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
     __syncthreads();
     {
       // wave-uniform row base plus a 32-bit per-lane offset (row 4 hh, column c); the
-      // per-register row steps (8 (i/4) + i%4) * stride are uniform too
+      // per-register row steps (8 (i/4) + i%4) * stride are uniform too. Every lane issues
+      // exactly kAtomicsPerTile atomics (the count the next tile's vmcnt wait assumes): a row
+      // past T adds 0 to row T - 1 instead.
       const int64_t qblk = q0 + 32 * qb;
       float* dqu = dQb + qblk * p.dq_strideM + 32 * dbq;
       const int loff = static_cast<int>(4 * hh * p.dq_strideM) + c;
-      const bool rows_in = qblk + 32 <= T;
+      const int rows_left = T - qblk < 32 ? static_cast<int>(T - qblk) : 32;  // rows < T
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         if ((i >> 3) != kh) continue;  // wave-uniform
         const int rs = row_of(i);
-        if (rows_in || qblk + 4 * hh + rs < T)
-          unsafeAtomicAdd(dqu + rs * p.dq_strideM + loff, (dq[i] + pbase[rs * 33]) * p.scale);
+        const bool in = 4 * hh + rs < rows_left;
+        const float v = in ? (dq[i] + pbase[rs * 33]) * p.scale : 0.f;
+        float* dst = in ? dqu + rs * p.dq_strideM + loff
+                        : dQb + (T - 1) * p.dq_strideM + 32 * dbq + c;
+        unsafeAtomicAdd(dst, v);
       }
     }
   }
@@ -478,6 +559,7 @@ extern "C" hipError_t hk_attn_backward(const hk_attn_bwd_params* params, int hea
   const int64_t bh = static_cast<int64_t>(p.B) * p.nh;
   HK_CHECK_ARG(bh <= 65535);
   HK_CHECK_ARG(p.dq_strideM >= 0 && p.dq_strideM < (int64_t{1} << 28));  // 32-bit lane offsets
+  HK_CHECK_ARG(p.T <= (1 << 24));  // 32-bit plane offsets
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
@@ -488,7 +570,22 @@ extern "C" hipError_t hk_attn_backward(const hk_attn_bwd_params* params, int hea
   HK_RETURN_IF_ERROR(attr);
   const int64_t nkt = (static_cast<int64_t>(p.T) + kBKV - 1) / kBKV;
   HK_CHECK_ARG(nkt * bh <= INT32_MAX);
+  // the query-side planes in the stream's workspace: 4 x [b, h][T][64] bf16, 2 x [b, h][T] fp32
+  const int64_t rows = bh * p.T;
+  const size_t plane = static_cast<size_t>(rows) * kRowBytes;
+  void* ws = nullptr;
+  HK_RETURN_IF_ERROR(hk::device_workspace(4 * plane + 2 * static_cast<size_t>(rows) * 4, stream,
+                                          &ws));
+  char* wsb = static_cast<char*>(ws);
+  float* l2 = reinterpret_cast<float*>(wsb + 4 * plane);
+  hipLaunchKernelGGL(attn_bwd_prepare,
+                     dim3(static_cast<unsigned>(hk::ceil_div(static_cast<int64_t>(p.T) * 8, 256)),
+                          static_cast<unsigned>(bh)),
+                     dim3(256), 0, stream, p, wsb, wsb + plane, wsb + 2 * plane, wsb + 3 * plane, l2,
+                     l2 + rows);
+  HK_RETURN_IF_ERROR(hk::launch_status());
+  const QPlanes qp{wsb, wsb + plane, wsb + 2 * plane, wsb + 3 * plane, l2, l2 + rows};
   hipLaunchKernelGGL(attn_bwd_kernel, dim3(static_cast<unsigned>(nkt * bh)), dim3(kThreads),
-                     kLdsBytes, stream, p, static_cast<int>(bh));
+                     kLdsBytes, stream, p, static_cast<int>(bh), qp);
   return hk::launch_status();
 }
