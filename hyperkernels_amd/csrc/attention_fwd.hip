@@ -111,7 +111,19 @@ __device__ __forceinline__ f32x16_t mfma3(bf16x8_t ah, bf16x8_t al, bf16x8_t bh,
 // K/V tile staging: thread t owns key rows 2 (t / 16) and 2 (t / 16) + 1 at d = 4 (t % 16) .. + 3
 // of both K and V (four 16-byte global loads, coalesced 256 bytes per 16 threads). K is split and
 // written as it lies; V is split and written transposed, the two keys of a d packed in one 32-bit
-// store.
+// store. Rows are permuted in LDS so that both stores are free of bank conflicts, and the
+// operand reads apply the same permutations:
+//   - key k of K sits in row k_slot(k), k with bits 1 and 3 exchanged: the 32 lanes of one
+//     8-byte store cycle write keys 4 u + j and 4 u + 2 + j, which then lie 8 rows (32 banks at
+//     the 144-byte pitch) apart instead of 2 rows (24 of their 32 banks shared); the 16 keys of
+//     one operand read cycle still fill 16 distinct rows mod 16;
+//   - d row of V^T sits in row vt_slot(d) = d ^ 2 for d >= 32: the lanes storing d >= 32
+//     (t % 16 >= 8) then sit 4 banks away from the lanes t % 16 - 8 at the 72-byte pitch instead
+//     of on the same bank.
+__device__ __forceinline__ int k_slot(int k) {
+  return (k & ~0xA) | (((k >> 1) & 1) << 3) | (((k >> 3) & 1) << 1);
+}
+__device__ __forceinline__ int vt_slot(int d) { return d ^ (d >> 4 & 2); }
 struct KVLoader {
   const float* k0p;  // this thread's first K row (key 2 (t / 16)) at its column
   const float* v0p;
@@ -156,7 +168,7 @@ struct KVLoader {
       const int key = 2 * pr + j;
       const u32x2_t s0 = split2(rk[j].x, rk[j].y), s1 = split2(rk[j].z, rk[j].w);
       const u32x2_t h = {s0.x, s1.x}, l = {s0.y, s1.y};
-      const int off = key * kKPitch + d0 * 2;
+      const int off = k_slot(key) * kKPitch + d0 * 2;
       *reinterpret_cast<u32x2_t*>(kh + off) = h;
       *reinterpret_cast<u32x2_t*>(kl + off) = l;
     }
@@ -167,7 +179,7 @@ struct KVLoader {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const u32x2_t hl = split2(a[i], c[i]);  // keys 2 pr and 2 pr + 1 of d0 + i
-      const int off = (d0 + i) * kVtPitch + 4 * pr;
+      const int off = vt_slot(d0 + i) * kVtPitch + 4 * pr;
       *reinterpret_cast<uint32_t*>(vh + off) = hl.x;
       *reinterpret_cast<uint32_t*>(vl + off) = hl.y;
     }
@@ -248,8 +260,8 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
                     p.V + b * p.v_strideB + h * p.v_strideH, p.k_strideM, p.v_strideM, T);
   f32x4_t rk[2], rv[2];
   // per-lane LDS offsets: K fragment (key c, d = 16 s + 8 hh), V^T fragments (row 32 db + c)
-  const int k_row = c * kKPitch + 16 * hh;
-  const int vt_row = c * kVtPitch + 8 * hh;
+  const int k_row = k_slot(c) * kKPitch + 16 * hh;
+  const int vt_row[2] = {vt_slot(c) * kVtPitch + 8 * hh, vt_slot(32 + c) * kVtPitch + 8 * hh};
   // a wave whose queries all precede key tile kt has nothing to add there (causal)
   auto active = [&](int kt) {
     return !p.is_causal || static_cast<int64_t>(kt) * kBKV <= q0w + 31;
@@ -337,7 +349,7 @@ __global__ __launch_bounds__(256, DROP ? 2 : 3) void attn_fwd_kernel(hk_attn_fwd
     auto vread = [&](int db) {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const int off = vt_row + 32 * db * kVtPitch + 32 * ks;
+        const int off = vt_row[db] + 32 * ks;
         const u32x2_t a0 = *reinterpret_cast<const u32x2_t*>(vh + off);
         const u32x2_t a1 = *reinterpret_cast<const u32x2_t*>(vh + off + 16);
         const u32x2_t b0 = *reinterpret_cast<const u32x2_t*>(vl + off);
