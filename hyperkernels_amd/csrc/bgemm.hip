@@ -47,15 +47,25 @@
 
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int BM = 256, BN = 256, BK = 64;             // BN: the full tile width
 constexpr int kStages = 2;                             // LDS ring depth (k-tiles)
 constexpr int kWaves = 8;                              // 2 x 4 over the tile, 2 per SIMD
 constexpr int kThreads = kWaves * 64;
-constexpr int kWaveM = 128, kWaveN = 64;               // 4 x 2 MFMA tiles of 32 x 32 per wave
-constexpr int kBlkM = kWaveM / 32, kBlkN = kWaveN / 32;
-constexpr int kStageBytes = 256 * BK * 2;              // one operand, one k-tile (32 KiB)
-constexpr int kLoadsPerWave = kStageBytes / 1024 / kWaves;  // 16-byte lane copies per operand per wave
-constexpr size_t kLdsBytes = static_cast<size_t>(kStages) * 2 * kStageBytes;  // 128 KiB
+constexpr int kWaveM = 128;                            // 4 MFMA tiles of 32 rows per wave
+constexpr int kBlkM = kWaveM / 32;
+constexpr int kStageBytes = 256 * BK * 2;              // the A operand, one k-tile (32 KiB)
+constexpr int kLoadsPerWave = kStageBytes / 1024 / kWaves;  // 16-byte lane copies of A per wave
+
+// Tile width BNT (256, or 128 for the half-width tiles that fill a last round, see
+// column_split): each wave owns 128 x BNT / 4 of C, kBlkN MFMA tiles of 32 columns.
+template <int BNT>
+struct TileN {
+  static constexpr int kWaveN = BNT / 4;
+  static constexpr int kBlkN = kWaveN / 32;
+  static constexpr int kStageBytesB = BNT * BK * 2;
+  static constexpr int kLoadsB = kStageBytesB / 1024 / kWaves;
+  static constexpr size_t kLdsBytes = static_cast<size_t>(kStages) * (kStageBytes + kStageBytesB);
+};
 
 typedef short bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short bf16x4_t __attribute__((ext_vector_type(4)));
@@ -90,16 +100,23 @@ __device__ __forceinline__ void copy16_to_lds(const void* sbase, int voff, unsig
 // bank half at 8 distinct chunk positions and the odd rows the other.
 //
 // M/N-major operands (element at base[k * ld + row]) are stored as in HBM, [64 k][256 rows]:
-// 512-byte k-rows whose 16-byte chunk c sits at c ^ (2 * (krow & 3)) ^ (8 * ((c >> 1) & 1)).
-// A copy instruction moves 2 k-rows (32 lanes read one contiguous 512-byte row segment). The
+// 512-byte k-rows (256 bytes for a 128-wide B tile) whose 16-byte chunk c sits at
+// c ^ (2 * (krow & 3)) ^ (8 * ((c >> 1) & 1)). Both row pitches are whole multiples of the 64
+// banks, so a chunk's banks depend on its stored position mod 16 alone and the placement below
+// holds for both. A copy instruction moves 2 k-rows (4 for 256-byte rows; 32 or 16 lanes read
+// one contiguous row segment). The
 // MFMA operand (8 consecutive k of one row/column) is gathered with two ds_read_b64_tr_b16:
 // within each 16-lane group, lane j reads 4 bf16 of k-row kb + j / 4 at columns
 // c0 + 4 (j % 4) and the hardware transposes the 16 x 4 block so lane i receives column
 // c0 + i, k = kb .. kb + 3. One group covers 4 k-rows x 32 bytes, which the (krow & 3) term
 // spreads over 32 banks; the two groups of a read cycle sit 16 columns (2 chunks) apart and
 // the (c >> 1) term places them in opposite bank halves.
-template <bool KMAJOR>
+template <bool KMAJOR, int ROWS = 256>
 struct TileOperand {
+  // M/N-major: a copy instruction (1 KiB) covers kRowsPerCopy k-rows of ROWS * 2 bytes.
+  static constexpr int kKRowBytes = ROWS * 2;
+  static constexpr int kRowsPerCopy = 1024 / kKRowBytes;
+  static constexpr int kLanesPerRow = 64 / kRowsPerCopy;
   // M/N-major: stored position of logical 16-byte chunk c of k-row krow, and its inverse.
   __device__ static int stored_chunk(int c, int krow) {
     return c ^ (2 * (krow & 3)) ^ (8 * ((c >> 1) & 1));
@@ -114,8 +131,8 @@ struct TileOperand {
       row = ii * 8 + (lane >> 3);
       k = ((lane & 7) ^ ((row >> 1) & 7)) * 8;
     } else {
-      k = ii * 2 + (lane >> 5);
-      row = logical_chunk(lane & 31, k) * 8;
+      k = ii * kRowsPerCopy + lane / kLanesPerRow;
+      row = logical_chunk(lane % kLanesPerRow, k) * 8;
     }
   }
   __device__ static int64_t byte_offset(int row, int k, int64_t ld) {
@@ -135,7 +152,7 @@ struct TileOperand {
       const int g = lane >> 4, j = lane & 15;
       const int col = wo + b * 32 + 16 * (g & 1) + 4 * (j & 3);
       const int krow = 16 * s + 8 * (g >> 1) + (j >> 2) + 4 * half;
-      return krow * 512 + stored_chunk(col >> 3, krow) * 16 + (col & 7) * 2;
+      return krow * kKRowBytes + stored_chunk(col >> 3, krow) * 16 + (col & 7) * 2;
     }
   }
   __device__ static bf16x8_t read(const unsigned char HK_LDS* st, int wo, int b, int s,
@@ -207,7 +224,7 @@ __device__ __forceinline__ void interleave_reads() {
 
 // Writes the 4 x 4 accumulator blocks of a wave: for block (i, j) and quad q, output row
 // row0 + 32 i and columns col0 + 32 j + 8 q .. +3 (one 8-byte store).
-template <bool BIAS>
+template <bool BIAS, int kBlkN>
 __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[kBlkM][kBlkN], const Epi& ep,
                                            uint16_t* Cb, int64_t ldc, int M, int N, int row0,
                                            int col0) {
@@ -251,24 +268,27 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[kBlkM][kBlkN], 
 // The operands are swapped in the MFMA (B block as the "A" input), so each lane ends up
 // holding 4 consecutive output columns of one output row per register quad: the epilogue
 // writes 8 bytes per quad straight from registers.
-template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL>
+// The kernel covers the columns [n_base, n_end) of C with BM x BNT tiles (N bounds the stores).
+template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL, int BNT>
 __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
     int M, int N, int K, Epi ep, const uint16_t* __restrict__ A, int64_t lda, int64_t sA,
     const uint16_t* __restrict__ B, int64_t ldb, int64_t sB, uint16_t* __restrict__ C,
     int64_t ldc, int64_t sC, int split_k, int k_per_split, float* __restrict__ part,
-    hk::F32Out fo) {
+    hk::F32Out fo, int n_base, int n_end) {
   using OA = TileOperand<A_KMAJOR>;
-  using OB = TileOperand<B_KMAJOR>;
+  using OB = TileOperand<B_KMAJOR, BNT>;
+  constexpr int kWaveN = TileN<BNT>::kWaveN, kBlkN = TileN<BNT>::kBlkN;
+  constexpr int kStageBytesB = TileN<BNT>::kStageBytesB, kLoadsB = TileN<BNT>::kLoadsB;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
   unsigned char HK_LDS* ldsA = (unsigned char HK_LDS*)lds_raw;
   unsigned char HK_LDS* ldsB = ldsA + kStages * kStageBytes;
 
   const int batch = blockIdx.z / split_k;
   const int split = blockIdx.z - batch * split_k;
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (n_end - n_base + BNT - 1) / BNT;
   int tm, tn;
   tile_coords(tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * BM, n0 = n_base + tn * BNT;
   const int kbeg = split * k_per_split;
   const int klen = min(K, kbeg + k_per_split) - kbeg;
 
@@ -285,8 +305,8 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
   const unsigned char* gB = reinterpret_cast<const unsigned char*>(
       B + static_cast<int64_t>(batch) * sB +
       (B_KMAJOR ? static_cast<int64_t>(n0) * ldb + kbeg : static_cast<int64_t>(kbeg) * ldb + n0));
-  int offA[kLoadsPerWave], offB[kLoadsPerWave];
-  int kA[kLoadsPerWave], kB[kLoadsPerWave];
+  int offA[kLoadsPerWave], offB[kLoadsB];
+  int kA[kLoadsPerWave], kB[kLoadsB];
 #pragma unroll
   for (int i = 0; i < kLoadsPerWave; ++i) {
     int row, k;
@@ -294,7 +314,11 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
     row = min(row, (A_KMAJOR ? M - 8 + 7 : M - 8) - m0);  // k-major: a row; else an 8-row chunk
     offA[i] = static_cast<int>(OA::byte_offset(row, k, lda));
     kA[i] = k;
-    OB::source(wave * kLoadsPerWave + i, lane, row, k);
+  }
+#pragma unroll
+  for (int i = 0; i < kLoadsB; ++i) {
+    int row, k;
+    OB::source(wave * kLoadsB + i, lane, row, k);
     row = min(row, (B_KMAJOR ? N - 8 + 7 : N - 8) - n0);
     offB[i] = static_cast<int>(OB::byte_offset(row, k, ldb));
     kB[i] = k;
@@ -305,15 +329,15 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
   const int ktiles = (klen + BK - 1) / BK;
   const bool tail = (klen % BK) != 0;  // last k-tile is partial
 
-  // Copy q (0 .. 2 * kLoadsPerWave - 1) of k-tile kt into ring slot `slot`. On a partial last
-  // k-tile (fill), lanes whose 8 k values lie past the split's end store zeros instead.
+  // Copy q (0 .. kLoadsPerWave + kLoadsB - 1) of k-tile kt into ring slot `slot`. On a partial
+  // last k-tile (fill), lanes whose 8 k values lie past the split's end store zeros instead.
   auto copy = [&](int kt, int slot, int q, bool fill) {
     const bool isA = q < kLoadsPerWave;
     const int i = isA ? q : q - kLoadsPerWave;
     const unsigned char* base = (isA ? gA + kt * stepA : gB + kt * stepB);
     const int off = isA ? offA[i] : offB[i];
-    const unsigned lds = (isA ? ldsA_addr : ldsB_addr) + slot * kStageBytes +
-                         (wave * kLoadsPerWave + i) * 1024;
+    const unsigned lds = isA ? ldsA_addr + slot * kStageBytes + (wave * kLoadsPerWave + i) * 1024
+                             : ldsB_addr + slot * kStageBytesB + (wave * kLoadsB + i) * 1024;
     if (!fill) {
       copy16_to_lds(base, off, lds);
     } else if (kt * BK + (isA ? kA[i] : kB[i]) < klen) {
@@ -324,7 +348,7 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
           u32x4_t{0u, 0u, 0u, 0u};
     }
   };
-  constexpr int kCopies = 2 * kLoadsPerWave;
+  constexpr int kCopies = kLoadsPerWave + kLoadsB;
 
   f32x16_t acc[kBlkM][kBlkN];
 #pragma unroll
@@ -361,7 +385,7 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
     const bool fill = !STEADY && tail && kt + kStages == ktiles - 1;
     const int slot = kt & 1;
     const unsigned char HK_LDS* sa = ldsA + slot * kStageBytes;
-    const unsigned char HK_LDS* sb = ldsB + slot * kStageBytes;
+    const unsigned char HK_LDS* sb = ldsB + slot * kStageBytesB;
 #pragma unroll
     for (int s = 0; s < BK / 16; ++s) {
       const int cur = s & 1, nxt = cur ^ 1;
@@ -382,7 +406,7 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
         __builtin_amdgcn_s_barrier();
         if (kt + 1 < ktiles) {
           const unsigned char HK_LDS* na = ldsA + (slot ^ 1) * kStageBytes;
-          const unsigned char HK_LDS* nb = ldsB + (slot ^ 1) * kStageBytes;
+          const unsigned char HK_LDS* nb = ldsB + (slot ^ 1) * kStageBytesB;
 #pragma unroll
           for (int i = 0; i < kBlkM; ++i) fa[nxt][i] = OA::read(na, wm * kWaveM, i, 0, lane);
 #pragma unroll
@@ -471,9 +495,9 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
   }
   uint16_t* Cb = C + static_cast<int64_t>(batch) * sC;
   if (ep.bias)
-    store_tile<true>(acc, ep, Cb, ldc, M, N, row0, col0);
+    store_tile<true, kBlkN>(acc, ep, Cb, ldc, M, N, row0, col0);
   else
-    store_tile<false>(acc, ep, Cb, ldc, M, N, row0, col0);
+    store_tile<false, kBlkN>(acc, ep, Cb, ldc, M, N, row0, col0);
 }
 
 // C = alpha * sum_s part[s] + beta * C (split order), fp32 -> bf16.
@@ -552,43 +576,99 @@ float bf16_bits_to_float(hk_bf16 h) {
   return f;
 }
 
-template <bool AK, bool BKM, bool P>
+template <bool AK, bool BKM, bool P, int BNT>
 hipError_t launch_tiled(dim3 grid, hipStream_t stream, int M, int N, int K, const Epi& ep,
                         const uint16_t* A, int64_t lda, int64_t sA, const uint16_t* B,
                         int64_t ldb, int64_t sB, uint16_t* C, int64_t ldc,
-                        int64_t sC, int split_k, int kps, float* part,
-                        const hk::F32Out& fo = hk::F32Out{}) {
+                        int64_t sC, int split_k, int kps, float* part, const hk::F32Out& fo,
+                        int n_base, int n_end) {
+  constexpr size_t kLds = TileN<BNT>::kLdsBytes;
   static std::once_flag once;
   static hipError_t attr_status = hipSuccess;
   std::call_once(once, [] {
-    attr_status = hipFuncSetAttribute(reinterpret_cast<const void*>(&bgemm_tiled<AK, BKM, P>),
+    attr_status = hipFuncSetAttribute(reinterpret_cast<const void*>(&bgemm_tiled<AK, BKM, P, BNT>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      static_cast<int>(kLdsBytes));
+                                      static_cast<int>(kLds));
   });
   HK_RETURN_IF_ERROR(attr_status);
-  hipLaunchKernelGGL((bgemm_tiled<AK, BKM, P>), grid, dim3(kThreads), kLdsBytes, stream, M, N, K,
-                     ep, A, lda, sA, B, ldb, sB, C, ldc, sC, split_k, kps, part, fo);
+  hipLaunchKernelGGL((bgemm_tiled<AK, BKM, P, BNT>), grid, dim3(kThreads), kLds, stream, M, N,
+                     K, ep, A, lda, sA, B, ldb, sB, C, ldc, sC, split_k, kps, part, fo, n_base,
+                     n_end);
   return hk::launch_status();
 }
 
-template <bool P>
+template <bool P, int BNT>
 hipError_t dispatch_layout(bool ta, bool tb, dim3 grid, hipStream_t stream, int M, int N, int K,
                            const Epi& ep, const uint16_t* A, int64_t lda, int64_t sA,
                            const uint16_t* B, int64_t ldb, int64_t sB, uint16_t* C,
                            int64_t ldc, int64_t sC, int split_k, int kps, float* part,
-                           const hk::F32Out& fo = hk::F32Out{}) {
+                           const hk::F32Out& fo, int n_base, int n_end) {
   // A is k-major unless transposed; B is k-major only when transposed.
   if (!ta && !tb)
-    return launch_tiled<true, false, P>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
-                                        C, ldc, sC, split_k, kps, part, fo);
+    return launch_tiled<true, false, P, BNT>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
+                                             C, ldc, sC, split_k, kps, part, fo, n_base, n_end);
   if (!ta && tb)
-    return launch_tiled<true, true, P>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
-                                       C, ldc, sC, split_k, kps, part, fo);
+    return launch_tiled<true, true, P, BNT>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
+                                            C, ldc, sC, split_k, kps, part, fo, n_base, n_end);
   if (ta && !tb)
-    return launch_tiled<false, false, P>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
-                                         C, ldc, sC, split_k, kps, part, fo);
-  return launch_tiled<false, true, P>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
-                                      C, ldc, sC, split_k, kps, part, fo);
+    return launch_tiled<false, false, P, BNT>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
+                                              C, ldc, sC, split_k, kps, part, fo, n_base, n_end);
+  return launch_tiled<false, true, P, BNT>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
+                                           C, ldc, sC, split_k, kps, part, fo, n_base, n_end);
+}
+
+// Columns [0, n_split) of C take 256 x 256 tiles and [n_split, N) 256 x 128 tiles. One
+// workgroup runs per CU (its LDS ring is 128 KiB), so a launch takes ceil(tiles / CUs) rounds;
+// when the last round of 256-wide tiles would be partly empty, the trailing tile columns run
+// as twice as many 128-wide tiles, which fill a round of half the length (8192 x 5120: 640
+// tiles are 3 rounds, 512 tiles + 256 half tiles are 2.5). Costs in full-tile rounds, a half
+// tile counted as 0.55 of one; a split is taken only if it saves at least 3%. Returns N for
+// no split.
+int column_split(int M, int N, int work_per_tile) {
+  const int64_t cus = hk::device_cu_count();
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  auto rounds = [&](int64_t tiles) { return static_cast<double>(hk::ceil_div(tiles * work_per_tile, cus)); };
+  const double whole = rounds(tiles_m * tiles_n);
+  double best = whole;
+  int64_t best_c = 0;
+  for (int64_t c = 1; c <= tiles_n; ++c) {
+    const int64_t n_split = (tiles_n - c) * BN;
+    const double cost = rounds(tiles_m * (tiles_n - c)) +
+                        0.55 * rounds(tiles_m * hk::ceil_div(N - n_split, int64_t{128}));
+    if (cost < best) {
+      best = cost;
+      best_c = c;
+    }
+  }
+  if (best_c == 0 || best > 0.97 * whole) return N;
+  return static_cast<int>((tiles_n - best_c) * BN);
+}
+
+// The product over its column regions (column_split), one launch per region; grid.z covers
+// batches and splits. A split into partials (P with split_k > 1) keeps one region.
+template <bool P>
+hipError_t run_regions(bool ta, bool tb, int grid_z, hipStream_t stream, int M, int N, int K,
+                       const Epi& ep, const uint16_t* A, int64_t lda, int64_t sA,
+                       const uint16_t* B, int64_t ldb, int64_t sB, uint16_t* C, int64_t ldc,
+                       int64_t sC, int split_k, int kps, float* part, const hk::F32Out& fo) {
+  const int64_t tiles_m = (M + BM - 1) / BM;
+  const int n_split = split_k == 1 ? column_split(M, N, grid_z) : N;
+  if (n_split > 0) {
+    const dim3 grid(static_cast<unsigned>(tiles_m * ((n_split + BN - 1) / BN)), 1, grid_z);
+    const hipError_t e = dispatch_layout<P, 256>(ta, tb, grid, stream, M, N, K, ep, A, lda, sA,
+                                                 B, ldb, sB, C, ldc, sC, split_k, kps, part, fo,
+                                                 0, n_split);
+    HK_RETURN_IF_ERROR(e);
+  }
+  if (n_split < N) {
+    const dim3 grid(static_cast<unsigned>(tiles_m * hk::ceil_div(N - n_split, int64_t{128})), 1,
+                    grid_z);
+    const hipError_t e = dispatch_layout<P, 128>(ta, tb, grid, stream, M, N, K, ep, A, lda, sA,
+                                                 B, ldb, sB, C, ldc, sC, split_k, kps, part, fo,
+                                                 n_split, N);
+    HK_RETURN_IF_ERROR(e);
+  }
+  return hipSuccess;
 }
 
 // Split-K chosen by the library when the caller gives none: the split that minimises a simple
@@ -680,19 +760,17 @@ hipError_t bgemm_run(int transA, int transB, int M, int N, int K, hk_bf16 alpha_
   // k range per split rounded to the k-tile; `used` splits are not empty
   int used = 1, kps = K;
   hk::bgemm_split_plan(M, N, K, batchCount, splitK, &used, &kps);
-  HK_CHECK_ARG(tiles <= INT32_MAX && static_cast<int64_t>(batchCount) * used <= 65535);
-  if (used == 1) {
-    dim3 grid(static_cast<unsigned>(tiles), 1, batchCount);
-    return dispatch_layout<false>(ta, tb, grid, stream, M, N, K, ep, A, lda, strideA, B, ldb,
-                                  strideB, C, ldc, strideC, 1, K, nullptr);
-  }
+  HK_CHECK_ARG(2 * tiles <= INT32_MAX && static_cast<int64_t>(batchCount) * used <= 65535);
+  if (used == 1)
+    return run_regions<false>(ta, tb, batchCount, stream, M, N, K, ep, A, lda, strideA, B, ldb,
+                              strideB, C, ldc, strideC, 1, K, nullptr, hk::F32Out{});
   void* ws = nullptr;
   const size_t part_bytes = static_cast<size_t>(used) * batchCount * M * N * sizeof(float);
   HK_RETURN_IF_ERROR(hk::device_workspace(part_bytes, stream, &ws));
   float* part = static_cast<float*>(ws);
-  dim3 grid(static_cast<unsigned>(tiles), 1, batchCount * used);
-  HK_RETURN_IF_ERROR(dispatch_layout<true>(ta, tb, grid, stream, M, N, K, ep, A, lda, strideA,
-                                           B, ldb, strideB, C, ldc, strideC, used, kps, part));
+  HK_RETURN_IF_ERROR(run_regions<true>(ta, tb, batchCount * used, stream, M, N, K, ep, A, lda,
+                                       strideA, B, ldb, strideB, C, ldc, strideC, used, kps,
+                                       part, hk::F32Out{}));
   const int64_t total = static_cast<int64_t>(M) * N * batchCount;
   const dim3 fgrid(static_cast<unsigned>(hk::ceil_div(total, 1024)));
   if (total < (int64_t{1} << 31))
@@ -729,12 +807,11 @@ hipError_t bgemm_partials(bool ta, bool tb, int M, int N, int K, const hk_bf16* 
                ldb % 8 == 0 && sA % 8 == 0 && sB % 8 == 0 && hk::aligned16(A) &&
                hk::aligned16(B) && lda < (1 << 22) && ldb < (1 << 22));
   const int64_t tiles = static_cast<int64_t>((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  HK_CHECK_ARG(tiles <= INT32_MAX && static_cast<int64_t>(batch) * used <= 65535);
+  HK_CHECK_ARG(2 * tiles <= INT32_MAX && static_cast<int64_t>(batch) * used <= 65535);
   const Epi ep{1.0f, 0.0f, nullptr, 0, 0};
-  dim3 grid(static_cast<unsigned>(tiles), 1, batch * used);
   const F32Out fo = used == 1 && out ? *out : F32Out{};
-  return dispatch_layout<true>(ta, tb, grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB, nullptr,
-                               0, 0, used, kps, part, fo);
+  return run_regions<true>(ta, tb, batch * used, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
+                           nullptr, 0, 0, used, kps, part, fo);
 }
 
 }  // namespace hk

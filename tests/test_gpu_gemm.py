@@ -207,6 +207,24 @@ def test_bgemm_baseline_shape_sampled_rows(hk, orc, ta, tb):
     assert rel <= 1e-2
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_bgemm_half_width_tail_tiles(hk, orc, ta, tb):
+    # 32 x 20 = 640 output tiles of 256 x 256 would leave half of a third round empty: the
+    # library runs the last 4 tile columns (from column 4096) as 256 x 128 tiles, the last of
+    # them 120 wide (N = 5112), with a partial last k-tile (K = 136). Rows over every tile row
+    # in full, so both column regions and their boundary are checked.
+    M, N, K = 8192, 5112, 136
+    say("bgemm half-width tail", ta, tb)
+    A, B, C0 = _operands(orc, M, N, K, ta, tb, 900)
+    out = _run(hk, "hk_bgemm", A, B, C0, M, N, K, ta, tb, 1.0, 0.5)
+    rows = _tile_rows(M)
+    Asub = np.ascontiguousarray(A[:, rows] if ta else A[rows, :])
+    ref = orc.bgemm(ta, tb, Asub, B, alpha=1.0, beta=0.5, C0=np.ascontiguousarray(C0[rows]))
+    rel = max_rel(orc.bf16_to_f32(out[rows]), ref)
+    print(f"half-width tail rel {rel:.2e}")
+    assert rel <= 1e-2
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
 def test_bgemm_partial_last_round_deterministic(hk, orc, ta, tb):
     # 17 x 17 = 289 output tiles (a last round of 33 on 256 CUs), 17 k-tiles, the last partial.
