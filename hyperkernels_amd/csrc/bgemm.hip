@@ -71,6 +71,7 @@ typedef short bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 #define HK_LDS __attribute__((address_space(3)))
 
@@ -257,6 +258,66 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[kBlkM][kBlkN], 
         __builtin_memcpy(&v.y, &bhi, 4);
         *dst = v;
       }
+  }
+}
+
+// Writes the accumulators of a wave through LDS, one 32-row MFMA block row at a time: the
+// wave stores its block row into its own fp32 staging area (32 rows, pitch kWaveN * 4 + 16
+// bytes, so the 16 lanes of one 16-byte write cycle start 4 banks apart), reads it back as 8
+// consecutive columns per lane and writes C with 16-byte stores, kWaveN / 8 lanes covering
+// one row segment (a whole 128-byte line for 64 columns). Stored straight from the MFMA
+// layout, every 8-byte store would touch 32 rows and every line of C would be assembled from 8
+// of them: 23% of the BASELINE product. The area is the wave's own, so it needs no barrier
+// beyond the one that ends the main loop. The epilogue arithmetic is that of store_tile.
+template <bool BIAS, int kWaveN>
+__device__ __forceinline__ void store_tile_staged(const f32x16_t (&acc)[kBlkM][kWaveN / 32],
+                                                  const Epi& ep, uint16_t* Cb, int64_t ldc,
+                                                  int M, int N, int wrow0, int wcol0,
+                                                  unsigned char HK_LDS* area, int lane) {
+  constexpr int kBlkN = kWaveN / 32;
+  constexpr int P = kWaveN * 4 + 16;        // staging pitch (bytes)
+  constexpr int LPR = kWaveN / 8;           // lanes per row
+  constexpr int RPP = 64 / LPR;             // rows per pass
+  const int r = lane & 31, h = lane >> 5;
+  const int rr0 = lane / LPR, cc = (lane % LPR) * 8;
+#pragma unroll
+  for (int i = 0; i < kBlkM; ++i) {
+#pragma unroll
+    for (int j = 0; j < kBlkN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<f32x4_t HK_LDS*>(area + r * P + (32 * j + 8 * q + 4 * h) * 4) =
+            f32x4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                    acc[i][j][4 * q + 3]};
+#pragma unroll
+    for (int p = 0; p < 32 / RPP; ++p) {
+      const int rr = p * RPP + rr0;
+      const f32x4_t a = *reinterpret_cast<const f32x4_t HK_LDS*>(area + rr * P + cc * 4);
+      const f32x4_t b = *reinterpret_cast<const f32x4_t HK_LDS*>(area + rr * P + cc * 4 + 16);
+      const int row = wrow0 + 32 * i + rr, col = wcol0 + cc;
+      if (row >= M || col >= N) continue;  // N % 8 == 0: the 8 columns are all in or all out
+      f32x2_t v[4] = {f32x2_t{a[0], a[1]} * ep.alpha, f32x2_t{a[2], a[3]} * ep.alpha,
+                      f32x2_t{b[0], b[1]} * ep.alpha, f32x2_t{b[2], b[3]} * ep.alpha};
+      uint4* dst = reinterpret_cast<uint4*>(Cb + static_cast<int64_t>(row) * ldc + col);
+      if (BIAS) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] += ep.beta * f32x2_t{bias_at(ep, row, col + 2 * e), bias_at(ep, row, col + 2 * e + 1)};
+      } else if (ep.beta != 0.0f) {
+        const uint4 old = *dst;
+        const uint32_t o[4] = {old.x, old.y, old.z, old.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] += ep.beta * f32x2_t{__uint_as_float(o[e] << 16), __uint_as_float(o[e] & 0xffff0000u)};
+      }
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bf16x2_t bv = __builtin_convertvector(v[e], bf16x2_t);
+        __builtin_memcpy(&w[e], &bv, 4);
+      }
+      *dst = make_uint4(w[0], w[1], w[2], w[3]);
+    }
   }
 }
 
@@ -494,10 +555,15 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
     return;
   }
   uint16_t* Cb = C + static_cast<int64_t>(batch) * sC;
+  // every wave is done with the LDS ring: its start becomes the waves' staging areas
+  static_assert(kWaves * 32 * (kWaveN * 4 + 16) <= TileN<BNT>::kLdsBytes, "staging fits");
+  __syncthreads();
+  unsigned char HK_LDS* area = ldsA + wave * (32 * (kWaveN * 4 + 16));
+  const int wrow0 = m0 + wm * kWaveM, wcol0 = n0 + wn * kWaveN;
   if (ep.bias)
-    store_tile<true, kBlkN>(acc, ep, Cb, ldc, M, N, row0, col0);
+    store_tile_staged<true, kWaveN>(acc, ep, Cb, ldc, M, N, wrow0, wcol0, area, lane);
   else
-    store_tile<false, kBlkN>(acc, ep, Cb, ldc, M, N, row0, col0);
+    store_tile_staged<false, kWaveN>(acc, ep, Cb, ldc, M, N, wrow0, wcol0, area, lane);
 }
 
 // C = alpha * sum_s part[s] + beta * C (split order), fp32 -> bf16.
