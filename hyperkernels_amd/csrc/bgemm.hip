@@ -223,57 +223,18 @@ __device__ __forceinline__ void interleave_reads() {
   }
 }
 
-// Writes the 4 x 4 accumulator blocks of a wave: for block (i, j) and quad q, output row
-// row0 + 32 i and columns col0 + 32 j + 8 q .. +3 (one 8-byte store).
-template <bool BIAS, int kBlkN>
-__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[kBlkM][kBlkN], const Epi& ep,
-                                           uint16_t* Cb, int64_t ldc, int M, int N, int row0,
-                                           int col0) {
-#pragma unroll
-  for (int i = 0; i < kBlkM; ++i) {
-    const int row = row0 + 32 * i;
-    if (row >= M) continue;
-    uint16_t* crow = Cb + static_cast<int64_t>(row) * ldc;
-#pragma unroll
-    for (int j = 0; j < kBlkN; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int col = col0 + 32 * j + 8 * q;
-        if (col >= N) continue;
-        f32x2_t lo = f32x2_t{acc[i][j][4 * q], acc[i][j][4 * q + 1]} * ep.alpha;
-        f32x2_t hi = f32x2_t{acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]} * ep.alpha;
-        uint2* dst = reinterpret_cast<uint2*>(crow + col);
-        if (BIAS) {
-          lo += ep.beta * f32x2_t{bias_at(ep, row, col), bias_at(ep, row, col + 1)};
-          hi += ep.beta * f32x2_t{bias_at(ep, row, col + 2), bias_at(ep, row, col + 3)};
-        } else if (ep.beta != 0.0f) {
-          const uint2 old = *dst;
-          lo += ep.beta * f32x2_t{__uint_as_float(old.x << 16), __uint_as_float(old.x & 0xffff0000u)};
-          hi += ep.beta * f32x2_t{__uint_as_float(old.y << 16), __uint_as_float(old.y & 0xffff0000u)};
-        }
-        const bf16x2_t blo = __builtin_convertvector(lo, bf16x2_t);
-        const bf16x2_t bhi = __builtin_convertvector(hi, bf16x2_t);
-        uint2 v;
-        __builtin_memcpy(&v.x, &blo, 4);
-        __builtin_memcpy(&v.y, &bhi, 4);
-        *dst = v;
-      }
-  }
-}
-
-// Writes the accumulators of a wave through LDS, one 32-row MFMA block row at a time: the
-// wave stores its block row into its own fp32 staging area (32 rows, pitch kWaveN * 4 + 16
-// bytes, so the 16 lanes of one 16-byte write cycle start 4 banks apart), reads it back as 8
-// consecutive columns per lane and writes C with 16-byte stores, kWaveN / 8 lanes covering
-// one row segment (a whole 128-byte line for 64 columns). Stored straight from the MFMA
-// layout, every 8-byte store would touch 32 rows and every line of C would be assembled from 8
-// of them: 23% of the BASELINE product. The area is the wave's own, so it needs no barrier
-// beyond the one that ends the main loop. The epilogue arithmetic is that of store_tile.
-template <bool BIAS, int kWaveN>
-__device__ __forceinline__ void store_tile_staged(const f32x16_t (&acc)[kBlkM][kWaveN / 32],
-                                                  const Epi& ep, uint16_t* Cb, int64_t ldc,
-                                                  int M, int N, int wrow0, int wcol0,
-                                                  unsigned char HK_LDS* area, int lane) {
+// Hands the accumulators of a wave to `out` through LDS, one 32-row MFMA block row at a time:
+// the wave stores its block row into its own fp32 staging area (32 rows, pitch kWaveN * 4 + 16
+// bytes, so the 16 lanes of one 16-byte write cycle start 4 banks apart) and reads it back as 8
+// consecutive columns per lane: out(row, col, a, b) gets the wave-relative row and column of
+// values a[0..3], b[0..3], and kWaveN / 8 consecutive lanes hold one row segment, so the
+// outputs can be written 16 (bf16) or 32 (fp32) bytes per lane in whole lines. Stored straight
+// from the MFMA layout instead, every store touched 32 rows and each 128-byte line of C was
+// assembled from 8 stores (bf16): 23% of the BASELINE product. The area is the wave's own, so
+// it needs no barrier beyond the one that ends the main loop.
+template <int kWaveN, typename Out>
+__device__ __forceinline__ void staged_rows(const f32x16_t (&acc)[kBlkM][kWaveN / 32],
+                                            unsigned char HK_LDS* area, int lane, Out&& out) {
   constexpr int kBlkN = kWaveN / 32;
   constexpr int P = kWaveN * 4 + 16;        // staging pitch (bytes)
   constexpr int LPR = kWaveN / 8;           // lanes per row
@@ -294,32 +255,45 @@ __device__ __forceinline__ void store_tile_staged(const f32x16_t (&acc)[kBlkM][k
       const int rr = p * RPP + rr0;
       const f32x4_t a = *reinterpret_cast<const f32x4_t HK_LDS*>(area + rr * P + cc * 4);
       const f32x4_t b = *reinterpret_cast<const f32x4_t HK_LDS*>(area + rr * P + cc * 4 + 16);
-      const int row = wrow0 + 32 * i + rr, col = wcol0 + cc;
-      if (row >= M || col >= N) continue;  // N % 8 == 0: the 8 columns are all in or all out
-      f32x2_t v[4] = {f32x2_t{a[0], a[1]} * ep.alpha, f32x2_t{a[2], a[3]} * ep.alpha,
-                      f32x2_t{b[0], b[1]} * ep.alpha, f32x2_t{b[2], b[3]} * ep.alpha};
-      uint4* dst = reinterpret_cast<uint4*>(Cb + static_cast<int64_t>(row) * ldc + col);
-      if (BIAS) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          v[e] += ep.beta * f32x2_t{bias_at(ep, row, col + 2 * e), bias_at(ep, row, col + 2 * e + 1)};
-      } else if (ep.beta != 0.0f) {
-        const uint4 old = *dst;
-        const uint32_t o[4] = {old.x, old.y, old.z, old.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          v[e] += ep.beta * f32x2_t{__uint_as_float(o[e] << 16), __uint_as_float(o[e] & 0xffff0000u)};
-      }
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bf16x2_t bv = __builtin_convertvector(v[e], bf16x2_t);
-        __builtin_memcpy(&w[e], &bv, 4);
-      }
-      *dst = make_uint4(w[0], w[1], w[2], w[3]);
+      out(32 * i + rr, cc, a, b);
     }
   }
 }
+
+// The bf16 epilogue on staged rows: C = alpha * acc + beta * C (or + beta * bias) in fp32,
+// one rounding to bf16 (v_cvt_pk_bf16_f32, round to nearest even), 16-byte stores.
+template <bool BIAS>
+struct Bf16RowOut {
+  const Epi& ep;
+  uint16_t* Cb;
+  int64_t ldc;
+  int M, N, wrow0, wcol0;
+  __device__ void operator()(int rr, int cc, const f32x4_t& a, const f32x4_t& b) const {
+    const int row = wrow0 + rr, col = wcol0 + cc;
+    if (row >= M || col >= N) return;  // N % 8 == 0: the 8 columns are all in or all out
+    f32x2_t v[4] = {f32x2_t{a[0], a[1]} * ep.alpha, f32x2_t{a[2], a[3]} * ep.alpha,
+                    f32x2_t{b[0], b[1]} * ep.alpha, f32x2_t{b[2], b[3]} * ep.alpha};
+    uint4* dst = reinterpret_cast<uint4*>(Cb + static_cast<int64_t>(row) * ldc + col);
+    if (BIAS) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] += ep.beta * f32x2_t{bias_at(ep, row, col + 2 * e), bias_at(ep, row, col + 2 * e + 1)};
+    } else if (ep.beta != 0.0f) {
+      const uint4 old = *dst;
+      const uint32_t o[4] = {old.x, old.y, old.z, old.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] += ep.beta * f32x2_t{__uint_as_float(o[e] << 16), __uint_as_float(o[e] & 0xffff0000u)};
+    }
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bf16x2_t bv = __builtin_convertvector(v[e], bf16x2_t);
+      __builtin_memcpy(&w[e], &bv, 4);
+    }
+    *dst = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
 
 // Main loop per k-tile kt (ring slot kt % 2), 4 k steps of 16 MFMAs each:
 //   steps 0-2: operands of step s+1 are read from LDS between the MFMAs of step s;
@@ -500,70 +474,54 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
   for (; kt < ktiles; ++kt) ktile(kt, std::false_type{});
 
   // Epilogue. Lane l holds, for MFMA block (i, j) and quad q, output row
-  // wm*128 + 32 i + l % 32 and columns wn*128 + 32 j + 8 q + 4 (l / 32) .. +3.
-  const int row0 = m0 + wm * kWaveM + (lane & 31);
-  const int col0 = n0 + wn * kWaveN + 4 * (lane >> 5);
-  if (PARTIAL && fo.C) {
-    // one split: fp32 C with alpha, beta and the bias applied here
-    float* cb = fo.C + static_cast<int64_t>(batch) * fo.sC;
-#pragma unroll
-    for (int i = 0; i < kBlkM; ++i) {
-      const int row = row0 + 32 * i;
-      if (row >= M) continue;
-#pragma unroll
-      for (int j = 0; j < kBlkN; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int col = col0 + 32 * j + 8 * q;
-          if (col >= N) continue;
-          float4* dst = reinterpret_cast<float4*>(cb + static_cast<int64_t>(row) * fo.ldc + col);
-          float4 v = make_float4(fo.alpha * acc[i][j][4 * q], fo.alpha * acc[i][j][4 * q + 1],
-                                 fo.alpha * acc[i][j][4 * q + 2], fo.alpha * acc[i][j][4 * q + 3]);
-          if (fo.beta != 0.0f) {
-            const float4 o = *dst;
-            v.x += fo.beta * o.x; v.y += fo.beta * o.y; v.z += fo.beta * o.z; v.w += fo.beta * o.w;
-          }
-          if (fo.bias) {
-            v.x += fo.bias_scale * f32out_bias(fo, M, N, batch, col);
-            v.y += fo.bias_scale * f32out_bias(fo, M, N, batch, col + 1);
-            v.z += fo.bias_scale * f32out_bias(fo, M, N, batch, col + 2);
-            v.w += fo.bias_scale * f32out_bias(fo, M, N, batch, col + 3);
-          }
-          *dst = v;
-        }
-    }
-    return;
-  }
-  if (PARTIAL) {
-    float* out = part + (static_cast<int64_t>(split) * (gridDim.z / split_k) + batch) *
-                            static_cast<int64_t>(M) * N;
-#pragma unroll
-    for (int i = 0; i < kBlkM; ++i) {
-      const int row = row0 + 32 * i;
-      if (row >= M) continue;
-#pragma unroll
-      for (int j = 0; j < kBlkN; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int col = col0 + 32 * j + 8 * q;
-          if (col < N)
-            *reinterpret_cast<float4*>(out + static_cast<int64_t>(row) * N + col) =
-                make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                            acc[i][j][4 * q + 3]);
-        }
-    }
-    return;
-  }
-  uint16_t* Cb = C + static_cast<int64_t>(batch) * sC;
+  // wm*128 + 32 i + l % 32 and columns wn*kWaveN + 32 j + 8 q + 4 (l / 32) .. +3; the rows go
+  // out through LDS (staged_rows).
   // every wave is done with the LDS ring: its start becomes the waves' staging areas
   static_assert(kWaves * 32 * (kWaveN * 4 + 16) <= TileN<BNT>::kLdsBytes, "staging fits");
   __syncthreads();
   unsigned char HK_LDS* area = ldsA + wave * (32 * (kWaveN * 4 + 16));
   const int wrow0 = m0 + wm * kWaveM, wcol0 = n0 + wn * kWaveN;
+  if (PARTIAL && fo.C) {
+    // one split: fp32 C with alpha, beta and the bias applied here
+    float* cb = fo.C + static_cast<int64_t>(batch) * fo.sC;
+    staged_rows<kWaveN>(acc, area, lane, [&](int rr, int cc, const f32x4_t& a, const f32x4_t& b) {
+      const int row = wrow0 + rr, col = wcol0 + cc;
+      if (row >= M || col >= N) return;  // N % 8 == 0
+      f32x4_t* dst = reinterpret_cast<f32x4_t*>(cb + static_cast<int64_t>(row) * fo.ldc + col);
+      f32x4_t v0 = fo.alpha * a, v1 = fo.alpha * b;
+      if (fo.beta != 0.0f) {
+        v0 += fo.beta * dst[0];
+        v1 += fo.beta * dst[1];
+      }
+      if (fo.bias) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v0[e] += fo.bias_scale * f32out_bias(fo, M, N, batch, col + e);
+          v1[e] += fo.bias_scale * f32out_bias(fo, M, N, batch, col + 4 + e);
+        }
+      }
+      dst[0] = v0;
+      dst[1] = v1;
+    });
+    return;
+  }
+  if (PARTIAL) {
+    float* out = part + (static_cast<int64_t>(split) * (gridDim.z / split_k) + batch) *
+                            static_cast<int64_t>(M) * N;
+    staged_rows<kWaveN>(acc, area, lane, [&](int rr, int cc, const f32x4_t& a, const f32x4_t& b) {
+      const int row = wrow0 + rr, col = wcol0 + cc;
+      if (row >= M || col >= N) return;
+      f32x4_t* dst = reinterpret_cast<f32x4_t*>(out + static_cast<int64_t>(row) * N + col);
+      dst[0] = a;
+      dst[1] = b;
+    });
+    return;
+  }
+  uint16_t* Cb = C + static_cast<int64_t>(batch) * sC;
   if (ep.bias)
-    store_tile_staged<true, kWaveN>(acc, ep, Cb, ldc, M, N, wrow0, wcol0, area, lane);
+    staged_rows<kWaveN>(acc, area, lane, Bf16RowOut<true>{ep, Cb, ldc, M, N, wrow0, wcol0});
   else
-    store_tile_staged<false, kWaveN>(acc, ep, Cb, ldc, M, N, wrow0, wcol0, area, lane);
+    staged_rows<kWaveN>(acc, area, lane, Bf16RowOut<false>{ep, Cb, ldc, M, N, wrow0, wcol0});
 }
 
 // C = alpha * sum_s part[s] + beta * C (split order), fp32 -> bf16.
