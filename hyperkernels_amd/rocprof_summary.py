@@ -8,7 +8,8 @@ Usage (after `rocprofv3 ... --output-format csv -d DIR -- python3 bench.py ...`)
         COPY_WRITE_DIR COPY_BYTES
         per-kernel HBM traffic per dispatch from FETCH_SIZE / WRITE_SIZE runs (KiB per dispatch),
         each scaled by the factor that makes the same counter read COPY_BYTES for a plain copy
-        kernel (torch's elementwise `mul(src, 1, out=dst)` over COPY_BYTES of float32).
+        kernel (torch's elementwise `mul(src, 1, out=dst)` over COPY_BYTES of float32): the
+        configs[1] step kernels by name, then every kernel symbol of the runs.
 
     python -m hyperkernels_amd.rocprof_summary pmc FILTER DIR [DIR ...]
         per kernel whose symbol contains FILTER: dispatches, mean duration and mean value per
@@ -110,6 +111,11 @@ def traffic(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_bytes):
         fb, wb = f[kf] * 1024.0 * f_scale, w[kw] * 1024.0 * w_scale
         lines.append(f"traffic: {name} fetch_bytes={fb:.0f} write_bytes={wb:.0f} "
                      f"traffic_bytes={fb + wb:.0f} raw_fetch_kib={f[kf]:.1f} raw_write_kib={w[kw]:.1f}")
+    # every kernel symbol of the runs (the step kernels above again, by symbol), per dispatch
+    for k in sorted(set(f) & set(w), key=lambda k: -(f[k] + w[k])):
+        fb, wb = f[k] * 1024.0 * f_scale, w[k] * 1024.0 * w_scale
+        lines.append(f"kernel {_short(k, 110)}: fetch_bytes={fb:.0f} write_bytes={wb:.0f} "
+                     f"traffic_bytes={fb + wb:.0f}")
     return lines
 
 
