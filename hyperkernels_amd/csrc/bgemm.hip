@@ -25,11 +25,14 @@
 //     placement of both is chosen through the per-lane source addresses of the copies.
 //   - Operand reads of the next k step are interleaved with the current step's MFMAs
 //     (sched_group_barrier), and the copies of the next tile with the last step's MFMAs.
-//   - Epilogue straight from registers: with the MFMA inputs swapped, each lane holds 4
-//     consecutive columns of one output row per accumulator quad; alpha / beta are applied in
-//     fp32 with one rounding to bf16 (v_cvt_pk_bf16_f32, round to nearest even) and 8 bytes
-//     are stored per quad (the reference rounds alpha * acc to bf16 and then blends beta * C
+//   - Epilogue through LDS: with the MFMA inputs swapped, each lane holds 4 consecutive
+//     columns of one output row per accumulator quad; each wave stages its rows in LDS and
+//     reads them back as 8 consecutive columns per lane. alpha / beta are applied in fp32 with
+//     one rounding to bf16 (v_cvt_pk_bf16_f32, round to nearest even) and 16 bytes are stored
+//     per lane, non-temporal (the reference rounds alpha * acc to bf16 and then blends beta * C
 //     in bf16 arithmetic).
+//   - Columns that would leave a last round of 256-wide tiles partly empty run as 128-wide
+//     tiles in the same launch (column_split, bgemm_mixed).
 //   - Edges: rows past M (N) are read clamped to the last row and their outputs are not
 //     stored; k past the end of the (split's) range is zero-filled in LDS on the last k-tile.
 //   - Workgroup order: consecutive tiles go to one XCD (the hardware deals workgroups to the 8
@@ -170,10 +173,11 @@ struct TileOperand {
   }
 };
 
-// Linear workgroup id -> (tile_m, tile_n): consecutive ids to one XCD, grouped 8 tile-rows.
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+// Linear tile id t -> (tile_m, tile_n): consecutive ids to one XCD, grouped 8 tile-rows. The
+// hardware deals workgroups to the 8 XCDs round-robin, so t % 8 is the XCD when t is a
+// workgroup id or one offset by a multiple of 8.
+__device__ __forceinline__ void tile_coords(int t, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int total = tiles_m * tiles_n;
-  int t = blockIdx.x;
   if ((total & 7) == 0) t = (t & 7) * (total >> 3) + (t >> 3);
   constexpr int G = 8;
   const int per_group = G * tiles_n;
@@ -291,7 +295,12 @@ struct Bf16RowOut {
       const bf16x2_t bv = __builtin_convertvector(v[e], bf16x2_t);
       __builtin_memcpy(&w[e], &bv, 4);
     }
-    *dst = make_uint4(w[0], w[1], w[2], w[3]);
+    // non-temporal: C is not read again by this product, and keeping it out of the caches
+    // leaves them to the operands (8192^3 NN: 742 -> 714 us on MI355X). The fp32 split-K
+    // partials below are read back by the finalize kernel and keep ordinary stores (with
+    // non-temporal ones the 8192 x 1280 x 5120 dA product went from 130 to 149 us).
+    typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(u32x4_t{w[0], w[1], w[2], w[3]}, reinterpret_cast<u32x4_t*>(dst));
   }
 };
 
@@ -301,15 +310,16 @@ struct Bf16RowOut {
 //              every wave done reading slot kt % 2), read step 0 of tile kt+1, and issue the
 //              copies of tile kt+2 into slot kt % 2 between the 16 MFMAs.
 // The operands are swapped in the MFMA (B block as the "A" input), so each lane ends up
-// holding 4 consecutive output columns of one output row per register quad: the epilogue
-// writes 8 bytes per quad straight from registers.
-// The kernel covers the columns [n_base, n_end) of C with BM x BNT tiles (N bounds the stores).
+// holding 4 consecutive output columns of one output row per register quad; the epilogue
+// hands them to the output through LDS (staged_rows).
+// One workgroup's tile: tile `wg` of the BM x BNT tiles that cover the columns
+// [n_base, n_end) of C (N bounds the stores).
 template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL, int BNT>
-__global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
-    int M, int N, int K, Epi ep, const uint16_t* __restrict__ A, int64_t lda, int64_t sA,
+__device__ __forceinline__ void tile_body(
+    int M, int N, int K, const Epi& ep, const uint16_t* __restrict__ A, int64_t lda, int64_t sA,
     const uint16_t* __restrict__ B, int64_t ldb, int64_t sB, uint16_t* __restrict__ C,
     int64_t ldc, int64_t sC, int split_k, int k_per_split, float* __restrict__ part,
-    hk::F32Out fo, int n_base, int n_end) {
+    const hk::F32Out& fo, int n_base, int n_end, int wg) {
   using OA = TileOperand<A_KMAJOR>;
   using OB = TileOperand<B_KMAJOR, BNT>;
   constexpr int kWaveN = TileN<BNT>::kWaveN, kBlkN = TileN<BNT>::kBlkN;
@@ -322,7 +332,7 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
   const int split = blockIdx.z - batch * split_k;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (n_end - n_base + BNT - 1) / BNT;
   int tm, tn;
-  tile_coords(tiles_m, tiles_n, tm, tn);
+  tile_coords(wg, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = n_base + tn * BNT;
   const int kbeg = split * k_per_split;
   const int klen = min(K, kbeg + k_per_split) - kbeg;
@@ -398,7 +408,12 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
 #pragma unroll
       for (int q = 0; q < kCopies; ++q) copy(p, p, q, fill);
     }
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  // Wait for k-tile 0 only; k-tile 1 lands while tile 0 is multiplied (waited for at its end).
+  // A partial (fill) k-tile 1 may have issued fewer copies than kCopies: wait for all then.
+  if (ktiles >= 2 && !(tail && ktiles == 2))
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kCopies) : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
 
   bf16x8_t fa[2][kBlkM], fb[2][kBlkN];
@@ -524,6 +539,39 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
     staged_rows<kWaveN>(acc, area, lane, Bf16RowOut<false>{ep, Cb, ldc, M, N, wrow0, wcol0});
 }
 
+// One column region: workgroup x takes tile x.
+template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL, int BNT>
+__global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
+    int M, int N, int K, Epi ep, const uint16_t* __restrict__ A, int64_t lda, int64_t sA,
+    const uint16_t* __restrict__ B, int64_t ldb, int64_t sB, uint16_t* __restrict__ C,
+    int64_t ldc, int64_t sC, int split_k, int k_per_split, float* __restrict__ part,
+    hk::F32Out fo, int n_base, int n_end) {
+  tile_body<A_KMAJOR, B_KMAJOR, PARTIAL, BNT>(M, N, K, ep, A, lda, sA, B, ldb, sB, C, ldc, sC,
+                                             split_k, k_per_split, part, fo, n_base, n_end,
+                                             blockIdx.x);
+}
+
+// Both column regions in one launch (column_split): workgroups [0, nfull) take the 256-wide
+// tiles of columns [0, n_split), the rest the 128-wide tiles of [n_split, N). The 128-wide
+// tiles start on CUs as the 256-wide ones finish, with no drain and launch between two
+// kernels (about 2% of the 8192 x 5120 x 1280 product on MI355X). nfull is a multiple of 8
+// whenever tile_coords' XCD grouping applies to both regions.
+template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL>
+__global__ __launch_bounds__(kThreads, 1) void bgemm_mixed(
+    int M, int N, int K, Epi ep, const uint16_t* __restrict__ A, int64_t lda, int64_t sA,
+    const uint16_t* __restrict__ B, int64_t ldb, int64_t sB, uint16_t* __restrict__ C,
+    int64_t ldc, int64_t sC, int split_k, int k_per_split, float* __restrict__ part,
+    hk::F32Out fo, int n_split, int nfull) {
+  const int wg = blockIdx.x;
+  if (wg < nfull)
+    tile_body<A_KMAJOR, B_KMAJOR, PARTIAL, 256>(M, N, K, ep, A, lda, sA, B, ldb, sB, C, ldc, sC,
+                                               split_k, k_per_split, part, fo, 0, n_split, wg);
+  else
+    tile_body<A_KMAJOR, B_KMAJOR, PARTIAL, 128>(M, N, K, ep, A, lda, sA, B, ldb, sB, C, ldc, sC,
+                                               split_k, k_per_split, part, fo, n_split, N,
+                                               wg - nfull);
+}
+
 // C = alpha * sum_s part[s] + beta * C (split order), fp32 -> bf16.
 // I: the index type, uint32_t when every index of the launch fits in 31 bits (a 64-bit
 // division costs several times a 32-bit one).
@@ -600,24 +648,32 @@ float bf16_bits_to_float(hk_bf16 h) {
   return f;
 }
 
+// BNT 256 or 128: one column region (bgemm_tiled); BNT 0: both regions (bgemm_mixed), with
+// n_base = n_split and n_end = nfull.
 template <bool AK, bool BKM, bool P, int BNT>
 hipError_t launch_tiled(dim3 grid, hipStream_t stream, int M, int N, int K, const Epi& ep,
                         const uint16_t* A, int64_t lda, int64_t sA, const uint16_t* B,
                         int64_t ldb, int64_t sB, uint16_t* C, int64_t ldc,
                         int64_t sC, int split_k, int kps, float* part, const hk::F32Out& fo,
                         int n_base, int n_end) {
-  constexpr size_t kLds = TileN<BNT>::kLdsBytes;
+  constexpr size_t kLds = TileN<BNT == 0 ? 256 : BNT>::kLdsBytes;
+  const void* fn;
+  if constexpr (BNT == 0) fn = reinterpret_cast<const void*>(&bgemm_mixed<AK, BKM, P>);
+  else fn = reinterpret_cast<const void*>(&bgemm_tiled<AK, BKM, P, BNT>);
   static std::once_flag once;
   static hipError_t attr_status = hipSuccess;
-  std::call_once(once, [] {
-    attr_status = hipFuncSetAttribute(reinterpret_cast<const void*>(&bgemm_tiled<AK, BKM, P, BNT>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+  std::call_once(once, [fn] {
+    attr_status = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       static_cast<int>(kLds));
   });
   HK_RETURN_IF_ERROR(attr_status);
-  hipLaunchKernelGGL((bgemm_tiled<AK, BKM, P, BNT>), grid, dim3(kThreads), kLds, stream, M, N,
-                     K, ep, A, lda, sA, B, ldb, sB, C, ldc, sC, split_k, kps, part, fo, n_base,
-                     n_end);
+  if constexpr (BNT == 0)
+    hipLaunchKernelGGL((bgemm_mixed<AK, BKM, P>), grid, dim3(kThreads), kLds, stream, M, N, K, ep,
+                       A, lda, sA, B, ldb, sB, C, ldc, sC, split_k, kps, part, fo, n_base, n_end);
+  else
+    hipLaunchKernelGGL((bgemm_tiled<AK, BKM, P, BNT>), grid, dim3(kThreads), kLds, stream, M, N,
+                       K, ep, A, lda, sA, B, ldb, sB, C, ldc, sC, split_k, kps, part, fo, n_base,
+                       n_end);
   return hk::launch_status();
 }
 
@@ -668,8 +724,8 @@ int column_split(int M, int N, int work_per_tile) {
   return static_cast<int>((tiles_n - best_c) * BN);
 }
 
-// The product over its column regions (column_split), one launch per region; grid.z covers
-// batches and splits. A split into partials (P with split_k > 1) keeps one region.
+// The product over its column regions (column_split), in one launch; grid.z covers batches
+// and splits. A split into partials (P with split_k > 1) keeps one region.
 template <bool P>
 hipError_t run_regions(bool ta, bool tb, int grid_z, hipStream_t stream, int M, int N, int K,
                        const Epi& ep, const uint16_t* A, int64_t lda, int64_t sA,
@@ -677,22 +733,22 @@ hipError_t run_regions(bool ta, bool tb, int grid_z, hipStream_t stream, int M, 
                        int64_t sC, int split_k, int kps, float* part, const hk::F32Out& fo) {
   const int64_t tiles_m = (M + BM - 1) / BM;
   const int n_split = split_k == 1 ? column_split(M, N, grid_z) : N;
-  if (n_split > 0) {
-    const dim3 grid(static_cast<unsigned>(tiles_m * ((n_split + BN - 1) / BN)), 1, grid_z);
-    const hipError_t e = dispatch_layout<P, 256>(ta, tb, grid, stream, M, N, K, ep, A, lda, sA,
-                                                 B, ldb, sB, C, ldc, sC, split_k, kps, part, fo,
-                                                 0, n_split);
-    HK_RETURN_IF_ERROR(e);
+  const int64_t nfull = tiles_m * ((n_split + BN - 1) / BN);
+  const int64_t nhalf = tiles_m * hk::ceil_div(N - n_split, int64_t{128});
+  if (nhalf == 0) {
+    const dim3 grid(static_cast<unsigned>(nfull), 1, grid_z);
+    return dispatch_layout<P, 256>(ta, tb, grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB, C,
+                                   ldc, sC, split_k, kps, part, fo, 0, N);
   }
-  if (n_split < N) {
-    const dim3 grid(static_cast<unsigned>(tiles_m * hk::ceil_div(N - n_split, int64_t{128})), 1,
-                    grid_z);
-    const hipError_t e = dispatch_layout<P, 128>(ta, tb, grid, stream, M, N, K, ep, A, lda, sA,
-                                                 B, ldb, sB, C, ldc, sC, split_k, kps, part, fo,
-                                                 n_split, N);
-    HK_RETURN_IF_ERROR(e);
+  if (nfull == 0) {
+    const dim3 grid(static_cast<unsigned>(nhalf), 1, grid_z);
+    return dispatch_layout<P, 128>(ta, tb, grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB, C,
+                                   ldc, sC, split_k, kps, part, fo, 0, N);
   }
-  return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(nfull + nhalf), 1, grid_z);
+  return dispatch_layout<P, 0>(ta, tb, grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB, C,
+                               ldc, sC, split_k, kps, part, fo, n_split,
+                               static_cast<int>(nfull));
 }
 
 // Split-K chosen by the library when the caller gives none: the split that minimises a simple
