@@ -120,7 +120,8 @@ __device__ __forceinline__ float ce_grad1(float v, float mx, float inv_sum, floa
   return (__expf(v - mx) * inv_sum - (hit ? 1.0f : 0.0f)) * scale;
 }
 
-// Vector path: logits and grad share the same 16-byte phase on every row. The row's body is cut
+// Row-chunk path (vocab < 4 * kFlatThreads; larger vocabularies take ce_backward_flat below):
+// logits and grad share the same 16-byte phase on every row. The row's body is cut
 // into chunks of kBwdThreads 16-byte vectors, one workgroup each (grid = rows x chunks), one
 // vector per lane: many short-lived workgroups keep more bytes in flight across the device
 // than a few long ones (measured on MI355X at 8192 x 50257: ~6.2 TB/s with 512-vector
@@ -164,6 +165,62 @@ __global__ __launch_bounds__(kBwdThreads) void ce_backward(
     o.z = ce_grad1(v.z, mx, inv_sum, scale, j + 2 == t);
     o.w = ce_grad1(v.w, mx, inv_sum, scale, j + 3 == t);
     hk::st_nt(gb + i, o);
+  }
+}
+
+// Flat path (vocab >= 4 * kFlatThreads): the [rows, vocab] logits as one stream of 16-byte
+// vectors from the first 16-byte boundary of the buffer, kFlatThreads vectors per workgroup,
+// one per lane. A workgroup's 4 * kFlatThreads elements then span at most two rows, whose
+// statistics it reads once; every element picks its row's by comparing its flat index with the
+// row boundary. With no row-aligned chunks there are no part-empty tail chunks and no per-row
+// head/tail work: 522 us against 541 us for the row chunks above at 8192 x 50257 on MI355X
+// (a plain 1-read/1-write copy of the same bytes: 500-511 us). Results are the same bits: the
+// per-element formula is ce_grad1 in both. The buffer's own head (before the first 16-byte
+// boundary, in row 0) and tail (after the last whole vector, in the last row) go to the first
+// and last workgroups' lanes.
+constexpr int kFlatThreads = 512;
+
+template <typename TIdx>
+__global__ __launch_bounds__(kFlatThreads) void ce_backward_flat(
+    const float* __restrict__ logits, const TIdx* __restrict__ targets,
+    float* __restrict__ grad, const float* __restrict__ saved_max,
+    const float* __restrict__ saved_sum, int64_t rows, int64_t vocab, int64_t head,
+    int64_t nvec, const float* __restrict__ grad_output, float host_scale) {
+  const int tid = threadIdx.x;
+  const int64_t v = static_cast<int64_t>(blockIdx.x) * kFlatThreads + tid;
+  const float4* xb = reinterpret_cast<const float4*>(logits + head);
+  float4 x;
+  if (v < nvec) x = hk::ld_nt(xb + v);  // issued before the row statistics are needed
+  const int64_t e0 = head + static_cast<int64_t>(blockIdx.x) * kFlatThreads * 4;
+  const int64_t r0 = e0 / vocab;
+  const int64_t r1 = min(r0 + 1, rows - 1);
+  const int64_t start1 = (r0 + 1) * vocab;  // flat index of row r0 + 1's first element
+  const float mx0 = saved_max[r0], inv0 = 1.0f / saved_sum[r0];
+  const float mx1 = saved_max[r1], inv1 = 1.0f / saved_sum[r1];
+  const int64_t t0 = static_cast<int64_t>(targets[r0]), t1 = static_cast<int64_t>(targets[r1]);
+  const float scale = (grad_output ? grad_output[0] : 1.0f) * host_scale;
+  if (blockIdx.x == 0 && tid < head)  // buffer head: row 0
+    grad[tid] = ce_grad1(logits[tid], mx0, inv0, scale, tid == t0);
+  if (blockIdx.x == gridDim.x - 1) {  // buffer tail: the last row
+    const int64_t j = head + 4 * nvec + tid;
+    if (j < rows * vocab) {
+      const int64_t rl = rows - 1;
+      grad[j] = ce_grad1(logits[j], saved_max[rl], 1.0f / saved_sum[rl], scale,
+                         j - rl * vocab == static_cast<int64_t>(targets[rl]));
+    }
+  }
+  if (v < nvec) {
+    const int64_t e = head + 4 * v;
+    const float xs[4] = {x.x, x.y, x.z, x.w};
+    float os[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bool second = e + c >= start1;
+      const int64_t col = e + c - (second ? start1 : start1 - vocab);
+      os[c] = ce_grad1(xs[c], second ? mx1 : mx0, second ? inv1 : inv0, scale,
+                       col == (second ? t1 : t0));
+    }
+    hk::st_nt(reinterpret_cast<float4*>(grad + head) + v, make_float4(os[0], os[1], os[2], os[3]));
   }
 }
 
@@ -211,6 +268,17 @@ hipError_t ce_backward_launch(const float* logits, const TIdx* targets, float* g
     hipLaunchKernelGGL(ce_backward_scalar<TIdx>, dim3(static_cast<unsigned>(batch_size)),
                        dim3(kThreads), 0, stream, logits, targets, grad, saved_max, saved_sum,
                        vocab_size, grad_output, host_scale);
+    return hk::launch_status();
+  }
+  if (vocab_size >= 4 * kFlatThreads) {
+    const int64_t total = batch_size * vocab_size;
+    const int64_t head = (4 - ((reinterpret_cast<uintptr_t>(logits) >> 2) & 3)) & 3;
+    const int64_t nvec = (total - head) / 4;
+    const int64_t blocks = hk::ceil_div(nvec, int64_t{kFlatThreads});
+    HK_CHECK_ARG(blocks <= INT32_MAX);
+    hipLaunchKernelGGL(ce_backward_flat<TIdx>, dim3(static_cast<unsigned>(blocks)),
+                       dim3(kFlatThreads), 0, stream, logits, targets, grad, saved_max, saved_sum,
+                       batch_size, vocab_size, head, nvec, grad_output, host_scale);
     return hk::launch_status();
   }
   // body vectors per row are at most vocab / 4; at least one chunk per row (head/tail only)
