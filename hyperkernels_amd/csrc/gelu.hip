@@ -10,16 +10,21 @@
 // gelu_backward_sm89_kernel.cu:88-90); 16-bit results are rounded to nearest even.
 //
 // HBM layout: flat contiguous tensors. Each lane moves 16 bytes per access (8 bf16 / fp16 or
-// 4 fp32) and a workgroup of 256 lanes covers kUnroll consecutive 4 KiB spans, so every wave
-// issues fully coalesced 1 KiB transactions. One span per workgroup (kUnroll = 1) measured
-// fastest on MI355X at the GPT-2 shape (25.2 M bf16: 22 us forward, 28.5 us backward, against
-// 30 / 33 us with four spans): many short workgroups ramp the device up and drain it faster.
+// 4 fp32), one vector per lane, so every wave issues fully coalesced 1 KiB transactions. One
+// vector per lane measured fastest on MI355X at the GPT-2 shape (25.2 M bf16: 22 us forward,
+// 28.5 us backward, against 30 / 33 us with four): many short workgroups ramp the device up
+// and drain it faster. Workgroup sizes from a sweep of plain streams at this size: the
+// 1-read / 1-write forward is fastest with 64 lanes (17.1 us against 17.9 us at 256), the
+// 2-read / 1-write backward with 512 (24.9 against 25.2 us); in the kernels, fp16 forward
+// 18.1 -> 17.3 us and backward 25.7 -> 25.5 us.
 #include "hk_device.h"
 #include "hk_host.h"
 
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;        // scalar kernels
+constexpr int kFwdVecThreads = 64;   // vector forward: 1 read, 1 write per vector
+constexpr int kBwdVecThreads = 512;  // vector backward: 2 reads, 1 write
 constexpr int kUnroll = 1;
 
 // With u = c (x + a x^3) (c = sqrt(2/pi), a = 0.044715, the Hendrycks & Gimpel tanh fit):
@@ -53,20 +58,20 @@ __device__ __forceinline__ float gelu_grad(float x) {
 }
 
 // Vector body: nvec 16-byte vectors, all pointers 16-byte aligned.
-template <typename T>
-__global__ __launch_bounds__(kThreads) void gelu_fwd_vec(const uint4* __restrict__ in,
-                                                         uint4* __restrict__ out, int64_t nvec) {
+template <typename T, int BS>
+__global__ __launch_bounds__(BS) void gelu_fwd_vec(const uint4* __restrict__ in,
+                                                   uint4* __restrict__ out, int64_t nvec) {
   constexpr int P = T::kPerVec;
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads * kUnroll + threadIdx.x;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * BS * kUnroll + threadIdx.x;
   uint4 r[kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = base + u * kThreads;
+    const int64_t i = base + u * BS;
     if (i < nvec) r[u] = hk::ld_nt(in + i);
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = base + u * kThreads;
+    const int64_t i = base + u * BS;
     if (i < nvec) {
       float f[P];
       T::unpack(r[u], f);
@@ -77,17 +82,16 @@ __global__ __launch_bounds__(kThreads) void gelu_fwd_vec(const uint4* __restrict
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) void gelu_bwd_vec(const uint4* __restrict__ grad,
-                                                         const uint4* __restrict__ in,
-                                                         uint4* __restrict__ grad_in,
-                                                         int64_t nvec) {
+template <typename T, int BS>
+__global__ __launch_bounds__(BS) void gelu_bwd_vec(const uint4* __restrict__ grad,
+                                                   const uint4* __restrict__ in,
+                                                   uint4* __restrict__ grad_in, int64_t nvec) {
   constexpr int P = T::kPerVec;
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads * kUnroll + threadIdx.x;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * BS * kUnroll + threadIdx.x;
   uint4 rg[kUnroll], rx[kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = base + u * kThreads;
+    const int64_t i = base + u * BS;
     if (i < nvec) {
       rg[u] = hk::ld_nt(grad + i);
       rx[u] = hk::ld_nt(in + i);
@@ -95,7 +99,7 @@ __global__ __launch_bounds__(kThreads) void gelu_bwd_vec(const uint4* __restrict
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = base + u * kThreads;
+    const int64_t i = base + u * BS;
     if (i < nvec) {
       float g[P], x[P];
       T::unpack(rg[u], g);
@@ -145,9 +149,10 @@ hipError_t launch_fwd(const S* in, S* out, int64_t numel, hipStream_t stream) {
   if (hk::aligned16(in) && hk::aligned16(out)) {
     const int64_t nvec = numel / P;
     if (nvec > 0) {
-      const int64_t blocks = hk::ceil_div(nvec, int64_t(kThreads) * kUnroll);
+      const int64_t blocks = hk::ceil_div(nvec, int64_t(kFwdVecThreads) * kUnroll);
       HK_CHECK_ARG(blocks <= INT32_MAX);
-      hipLaunchKernelGGL(gelu_fwd_vec<T>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+      hipLaunchKernelGGL((gelu_fwd_vec<T, kFwdVecThreads>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(kFwdVecThreads), 0,
                          stream, reinterpret_cast<const uint4*>(in),
                          reinterpret_cast<uint4*>(out), nvec);
       HK_RETURN_IF_ERROR(hk::launch_status());
@@ -173,9 +178,10 @@ hipError_t launch_bwd(const S* grad, const S* in, S* grad_in, int64_t numel,
   if (hk::aligned16(grad) && hk::aligned16(in) && hk::aligned16(grad_in)) {
     const int64_t nvec = numel / P;
     if (nvec > 0) {
-      const int64_t blocks = hk::ceil_div(nvec, int64_t(kThreads) * kUnroll);
+      const int64_t blocks = hk::ceil_div(nvec, int64_t(kBwdVecThreads) * kUnroll);
       HK_CHECK_ARG(blocks <= INT32_MAX);
-      hipLaunchKernelGGL(gelu_bwd_vec<T>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+      hipLaunchKernelGGL((gelu_bwd_vec<T, kBwdVecThreads>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(kBwdVecThreads), 0,
                          stream, reinterpret_cast<const uint4*>(grad),
                          reinterpret_cast<const uint4*>(in), reinterpret_cast<uint4*>(grad_in),
                          nvec);
