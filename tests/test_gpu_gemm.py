@@ -225,6 +225,48 @@ def test_bgemm_half_width_tail_tiles(hk, orc, ta, tb):
     assert rel <= 1e-2
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_bgemm_one_launch_ragged_rows(hk, orc, ta, tb):
+    # M = 8000: the last tile row of both tile widths is partial (rows 7936..7999) in the launch
+    # that runs the 256-wide and the 128-wide tiles together (N = 5112, K = 136 as above).
+    M, N, K = 8000, 5112, 136
+    say("bgemm one launch ragged rows", ta, tb)
+    A, B, C0 = _operands(orc, M, N, K, ta, tb, 950)
+    out = _run(hk, "hk_bgemm", A, B, C0, M, N, K, ta, tb, 1.0, 0.5)
+    rows = np.unique(np.concatenate([_tile_rows(M), np.arange(M - 64, M)]))
+    Asub = np.ascontiguousarray(A[:, rows] if ta else A[rows, :])
+    ref = orc.bgemm(ta, tb, Asub, B, alpha=1.0, beta=0.5, C0=np.ascontiguousarray(C0[rows]))
+    rel = max_rel(orc.bf16_to_f32(out[rows]), ref)
+    print(f"one launch ragged rows rel {rel:.2e}")
+    assert rel <= 1e-2
+
+
+def test_bgemm_one_launch_batched(hk, orc):
+    # Two batches of 4096 x 5120 (2 x 320 tiles of 256 x 256, so the last 4 tile columns of each
+    # batch run 128 wide in the same launch, grid.z = 2): each batch against its own product.
+    M, N, K, batch = 4096, 5120, 136, 2
+    say("bgemm one launch batched")
+    As, Bs, Cs = [], [], []
+    for b in range(batch):
+        A, B, C0 = _operands(orc, M, N, K, 0, 0, 960 + 10 * b)
+        As.append(A)
+        Bs.append(B)
+        Cs.append(C0)
+    dA, dB, dC = to_dev_bf16(np.stack(As)), to_dev_bf16(np.stack(Bs)), to_dev_bf16(np.stack(Cs))
+    lib = hk.lib()
+    assert lib.hk_bgemm_split_count(0, 0, M, N, K, batch, 0) == 1
+    st = lib.hk_bgemm(0, 0, M, N, K, bits(1.0), dA.data_ptr(), K, M * K, dB.data_ptr(), N, K * N,
+                      bits(0.5), dC.data_ptr(), N, M * N, batch,
+                      torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    out = to_host_bits(dC)
+    rows = _tile_rows(M)
+    for b in range(batch):
+        ref = orc.bgemm(0, 0, np.ascontiguousarray(As[b][rows, :]), Bs[b], alpha=1.0, beta=0.5,
+                        C0=np.ascontiguousarray(Cs[b][rows]))
+        assert max_rel(orc.bf16_to_f32(out[b][rows]), ref) <= 1e-2
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
 def test_bgemm_partial_last_round_deterministic(hk, orc, ta, tb):
     # 17 x 17 = 289 output tiles (a last round of 33 on 256 CUs), 17 k-tiles, the last partial.
