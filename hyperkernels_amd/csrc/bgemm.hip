@@ -554,8 +554,10 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
 // Both column regions in one launch (column_split): workgroups [0, nfull) take the 256-wide
 // tiles of columns [0, n_split), the rest the 128-wide tiles of [n_split, N). The 128-wide
 // tiles start on CUs as the 256-wide ones finish, with no drain and launch between two
-// kernels (about 2% of the 8192 x 5120 x 1280 product on MI355X). nfull is a multiple of 8
-// whenever tile_coords' XCD grouping applies to both regions.
+// kernels (about 2% of the 8192 x 5120 x 1280 product on MI355X). tile_coords' XCD grouping
+// of the 128-wide region assumes that its first workgroup sits on XCD 0, which holds when
+// nfull is a multiple of 8; otherwise only that region's L2 grouping is off, not which tiles
+// it covers.
 template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL>
 __global__ __launch_bounds__(kThreads, 1) void bgemm_mixed(
     int M, int N, int K, Epi ep, const uint16_t* __restrict__ A, int64_t lda, int64_t sA,
