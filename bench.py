@@ -661,6 +661,10 @@ def gemm_cases(g):
          lambda: torch.matmul(A_mk, B_nk.t(), out=C), flop, "bf16"),
         ("vendor_hipblaslt_bf16_TN_8192x5120x1280",
          lambda: torch.matmul(A_km.t(), B_kn, out=C), flop, "bf16"),
+        ("vendor_hipblaslt_bf16_dA_NT_8192x1280x5120",
+         lambda: torch.matmul(dY, B_kn.t(), out=dX), flop, "bf16"),
+        ("vendor_hipblaslt_bf16_dB_TN_1280x5120x8192",
+         lambda: torch.matmul(A_mk.t(), dY, out=dW), flop, "bf16"),
         ("vendor_hipblaslt_fp32_NN_4096^3_bias", lambda: torch.addmm(sbias, sa, sb, out=sc),
          W.gemm_flop(S["M"], S["N"], S["K"]), "fp32_matrix"),
     ]

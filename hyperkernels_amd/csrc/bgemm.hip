@@ -775,20 +775,36 @@ hipError_t run_regions(bool ta, bool tb, int grid_z, hipStream_t stream, int M, 
                                static_cast<int>(nfull));
 }
 
-// Split-K chosen by the library when the caller gives none: the split that minimises a simple
-// cost model of (rounds of 256 x 256 tiles over the CUs) x (k-tiles per split) plus the HBM
-// traffic of fp32 partials (written, then read back with one bf16 write by the finalize).
-// Few output tiles with a long K (e.g. the dB = X^T dY product, 100 tiles, 128 k-tiles) gain
-// most; the costs are per k-tile of one workgroup (~2.7 us) and ~5 TB/s for the partials.
+// Split-K chosen by the library when the caller gives none: the split with the least modelled
+// time (us), summed over the rounds of 256 x 256 work items on the CUs:
+//   - a round costs (k-tiles per split) x t(busy) plus a fixed prologue / epilogue (8 us with
+//     bf16 C, 12 us with a 256 KiB fp32 partial per tile);
+//   - t, a workgroup's time per k-tile, grows with the share of the CUs that are busy (clock
+//     and shared-cache headroom): ~0.875 us with 100 of 256 CUs busy, ~1.62 us with all;
+//   - splits add the finalize, an HBM pass over the partials (4 s + 2 bytes per output at
+//     ~6 TB/s).
+// Calibrated on the 8192 x 1280 x 5120 and 1280 x 5120 x 8192 products (160 and 100 tiles):
+// measured 123 / 149 / 131 us at 1 / 2 / 3 splits for the first, 120 / 115 / 151 / 137 / 135
+// us at 1 to 5 for the second; the model picks 1 and 2.
 int auto_split_k(int64_t work_tiles, int64_t ktiles, int64_t outputs) {
   const int64_t cus = hk::device_cu_count();
+  auto t_kt = [&](int64_t busy) {
+    const double f = static_cast<double>(busy) / static_cast<double>(cus);
+    const double x = (f - 0.39) / 0.61;
+    return 0.875 + 0.745 * (x < 0.0 ? 0.0 : x > 1.0 ? 1.0 : x);
+  };
   double best = 0.0;
   int best_s = 1;
   for (int s = 1; s <= 8; ++s) {
     if (s > 1 && ktiles / s < 4) break;
-    const double rounds = static_cast<double>(hk::ceil_div(work_tiles * s, cus));
-    double cost = rounds * static_cast<double>(hk::ceil_div(ktiles, static_cast<int64_t>(s))) * 2.7;
-    if (s > 1) cost += static_cast<double>(8 * s + 2) * static_cast<double>(outputs) / 5.0e6;
+    const int64_t items = work_tiles * s, kps = hk::ceil_div(ktiles, static_cast<int64_t>(s));
+    const double fixed = s > 1 ? 12.0 : 8.0;
+    double cost = 0.0;
+    for (int64_t done = 0; done < items; done += cus) {
+      const int64_t busy = items - done < cus ? items - done : cus;
+      cost += static_cast<double>(kps) * t_kt(busy) + fixed;
+    }
+    if (s > 1) cost += static_cast<double>(4 * s + 2) * static_cast<double>(outputs) / 6.0e6;
     if (s == 1 || cost < best) {
       best = cost;
       best_s = s;
