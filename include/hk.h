@@ -285,9 +285,10 @@ HK_API hipError_t hk_reduce_generic_f32(const float* src, float* dst, int out_nd
  * hk_bgemm_nt_backward (dA = dY * B^T) replaces bgemm_nt_backward_kernel
  *   (blas/bf16/bgemm_backward_nt_sm89_kernel.cu:23-32); hk_bgemm_tn_backward (dB = A^T * dY)
  *   replaces bgemm_tn_backward_kernel (blas/bf16/bgemm_backward_tn_sm89_kernel.cu:25-34).
- * hk_bgemm and the two backward entry points have no split argument (as in the reference); the
- *   library splits K itself when the output has too few 256 x 256 tiles to fill the device
- *   (same fp32 partials and split-order sum as hk_bgemm_core).
+ * hk_bgemm and the two backward entry points have no split argument (as in the reference); when
+ *   the output has too few 256 x 256 tiles to fill the device the library may split K itself,
+ *   where its cost model expects that to pay (same fp32 partials and split-order sum as
+ *   hk_bgemm_core).
  * hk_bgemm_split_count (no counterpart in the reference: a host-only planning query for callers
  *   and tests that check which plan runs) returns the number of k splits a product of this
  *   shape runs with (contiguous operands, 16-byte aligned): splitK = 0 for hk_bgemm and the
