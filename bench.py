@@ -842,6 +842,54 @@ def main():
                 if k in result["per_kernel"]:
                     result["per_kernel"][k]["cpu"] = e
     print(json.dumps(result), flush=True)
+    print_summary(result)
+
+
+# BASELINE.json's configs in order, each with the per-kernel entries that measure it
+SUMMARY = [
+    ("configs[0] LayerNorm fp32 4096x768",
+     ["ln_fwd", "ln_bwd_fused", "ln_bwd_input", "ln_bwd_gamma_beta"]),
+    ("configs[1] GELU bf16 / CE / AdamW (inside the step)",
+     ["gelu_fwd_bf16", "ce_fwd", "ce_bwd", "gelu_bwd_bf16", "adamw_148"]),
+    ("configs[2] attention fwd 8x12x1024x64",
+     ["attn_fwd_causal_8x12x1024x64", "attn_fwd_noncausal_8x12x1024x64"]),
+    ("configs[3] attention bwd 8x12x1024x64",
+     ["attn_bwd_causal_8x12x1024x64", "attn_bwd_noncausal_8x12x1024x64"]),
+    ("configs[4] BGEMM 8192x5120x1280 / SGEMM 4096^3",
+     ["bgemm_NN_8192x5120x1280", "bgemm_NT_8192x5120x1280", "bgemm_TN_8192x5120x1280",
+      "bgemm_TT_8192x5120x1280", "bgemm_dA_NT_8192x1280x5120", "bgemm_dB_TN_1280x5120x8192",
+      "sgemm_NN_4096^3_splitk4_bias", "sgemm_NN_4096^3_auto_split_bias"]),
+]
+
+
+def print_summary(result):
+    """The last lines on stderr: one short line per BASELINE config entry (time in us, rate,
+    fraction of the peak, the oracle's time on one thread and on all cores), so that a reader
+    of only the end of the log sees every config."""
+    per = result.get("per_kernel", {})
+    if not per:
+        return
+    short = {"_8x12x1024x64": "", "_8192x5120x1280": "", "_8192x1280x5120": "",
+             "_1280x5120x8192": "", "_4096^3": "", "_bias": ""}
+    lines = [f"[summary] headline {result['value']:.0f} GB/s, {result['ms_per_step']:.4f} ms/step; "
+             "name us rate frac cpu-1t/cpu-all ms"]
+    for title, names in SUMMARY:
+        lines.append(f"[summary] {title}")
+        for n in names:
+            e = per.get(n)
+            if e is None:
+                continue
+            label = n
+            for k, v in short.items():
+                label = label.replace(k, v)
+            ms = e.get("median_ms", e.get("avg_ms"))
+            unit = "G" if e.get("unit") == "GB/s" else "T"
+            cpu = e.get("cpu", {})
+            cpu_s = (f" {cpu['ms_1thread']:.4g}/{cpu['ms_all_cores']:.4g}"
+                     if "ms_1thread" in cpu else "")
+            lines.append(f"  {label} {ms * 1e3:.1f} {e['achieved']:.0f}{unit} "
+                         f"{e['frac']:.3f}{cpu_s}")
+    print("\n".join(lines), file=sys.stderr, flush=True)
 
 
 if __name__ == "__main__":

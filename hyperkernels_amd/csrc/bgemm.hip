@@ -86,8 +86,12 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 // kernel waits for the copies itself (vmcnt) before the barrier that publishes a stage.
 // Address = sbase (wave-uniform 64-bit, SGPRs) + voff (per-lane byte offset).
 __device__ __forceinline__ void copy16_to_lds(const void* sbase, int voff, unsigned lds_addr) {
-  // m0 (the LDS destination) is an input operand, so the compiler knows the asm sets it
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr));
+  // m0 (the LDS destination) is an input operand, so the compiler knows the asm sets it. Its
+  // hazard checks do not see inside the asm, so the asm supplies the wait states itself: an
+  // SALU write of m0 needs 1 before an LDS-DMA load, and an SGPR of sbase written by a VALU
+  // (v_readlane, when the compiler reloads a spilled SGPR) needs 5 before a VMEM read of it.
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+               "{m0}"(lds_addr));
 }
 
 // One operand of a k-tile in LDS: 256 rows of M (or N) by BK = 64 k, bf16, 32 KiB.

@@ -59,8 +59,12 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 // wait for all outstanding copies (the kernel orders them itself with vmcnt + barrier).
 // Address = sbase (wave-uniform 64-bit) + voff (per-lane byte offset).
 __device__ __forceinline__ void copy16_to_lds(const void* sbase, int voff, unsigned lds_addr) {
-  // m0 (the LDS destination) is an input operand, so the compiler knows the asm sets it
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr));
+  // m0 (the LDS destination) is an input operand, so the compiler knows the asm sets it. Its
+  // hazard checks do not see inside the asm, so the asm supplies the wait states itself: an
+  // SALU write of m0 needs 1 before an LDS-DMA load, and an SGPR of sbase written by a VALU
+  // (v_readlane, when the compiler reloads a spilled SGPR) needs 5 before a VMEM read of it.
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+               "{m0}"(lds_addr));
 }
 
 // One operand of a k-tile in LDS: 256 rows of M (or N) by BK = 32 k, fp32, 32 KiB.
@@ -429,11 +433,12 @@ __global__ __launch_bounds__(256) void sgemm_simple(int ta, int tb, int M, int N
 // thread (cols % 4 == 0, 16-byte aligned rows): one 16-byte load, three 8-byte stores; batch b
 // in blockIdx.y and a 32-bit index within one matrix (rows * cols / 4 < 2^31, checked by the
 // host). Runs at copy rate (a measured ~6.8 TB/s for 4096 x 4096).
-// Non-finite x (inf, NaN, or a finite value that rounds past bf16's largest one): hi carries
-// it, lo and hi' (the copy of hi in the cross term) are 0. The cross terms of its products are
-// then 0 and the product is hi * bh alone, +-inf or NaN as the reference's TF32 product is;
-// with lo = bf16(x - hi) and hi' = hi they would add inf * bl (NaN for bl = 0 or of the other
-// sign) and bf16(inf - inf) = NaN.
+// Non-finite x (inf, NaN): hi carries it, lo and hi' (the copy of hi in the cross term) are 0.
+// The cross terms of its products are then 0 and the product is hi * bh alone, +-inf or NaN as
+// the reference's TF32 product is; with lo = bf16(x - hi) and hi' = hi they would add inf * bl
+// (NaN for bl = 0 or of the other sign) and bf16(inf - inf) = NaN. A finite x that rounds past
+// bf16's largest value (|x| > (2 - 2^-8) 2^127) keeps hi = +-that largest value and
+// lo = bf16(x - hi), so it stays finite as it does in TF32 (whose range is fp32's).
 template <bool KCOLS>
 __global__ __launch_bounds__(256) void split3(const float* __restrict__ X, int64_t ldx, int64_t sx,
                                               int rows, int cols, uint16_t* __restrict__ Y,
@@ -449,6 +454,8 @@ __global__ __launch_bounds__(256) void split3(const float* __restrict__ X, int64
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     h[k] = hk::f32_to_bf16(v[k]);
+    const bool x_finite = (__float_as_uint(v[k]) & 0x7f800000u) != 0x7f800000u;
+    if (x_finite && (h[k] & 0x7f80u) == 0x7f80u) h[k] = (h[k] & 0x8000u) | 0x7f7fu;
     const bool finite = (h[k] & 0x7f80u) != 0x7f80u;
     l[k] = finite ? hk::f32_to_bf16(v[k] - hk::bf16_to_f32(h[k])) : uint16_t{0};
     hc[k] = finite ? h[k] : uint16_t{0};
@@ -584,6 +591,9 @@ hipError_t sgemm_run(bool ta, bool tb, int M, int N, int K, float alpha, const f
     const int64_t na = static_cast<int64_t>(M) * K3, nb = static_cast<int64_t>(K3) * N;
     int used = 1, kps = 0;
     hk::bgemm_split_plan(M, N, K3, batchCount, splitK, &used, &kps);
+    // the plan never exceeds the k-tile count; refuse a grid the tiles cannot take before
+    // anything is allocated or launched
+    HK_CHECK_ARG(static_cast<int64_t>(batchCount) * used <= 65535);
     auto up = [](int64_t bytes) { return (bytes + 255) & ~int64_t{255}; };
     const int64_t a_bytes = up(na * batchCount * 2), b_bytes = up(nb * batchCount * 2);
     // one split: the GEMM tiles write C themselves (alpha, beta, bias), no partials

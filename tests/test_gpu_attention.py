@@ -295,3 +295,35 @@ def test_attn_forward_dropout_baseline_shape_sampled_heads(hk, orc, causal):
                                   mask=mask[sl].cpu().numpy())
         assert max_rel(o[sl].cpu().numpy(), ro) <= 2e-3
         assert max_rel(lse[sl].cpu().numpy(), rl) <= 2e-3
+
+
+@pytest.mark.parametrize("T", [100, 256])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attn_backward_strided_bthd_layout(hk, orc, T, causal):
+    # [B, T, H, d] storage viewed as [B, H, T, d] for Q, K, V, dO and the dQ / dK / dV outputs,
+    # and LSE / D inside NaN-padded [B, H + 1, T + 5] buffers: every batch, head and row stride
+    # that the Q / dO pre-pass and the kernel read differs from the contiguous one.
+    B, H, D = 2, 3, 64
+    say("attn bwd strided", T, causal)
+    q, k, v, do = _qkv(orc, B, H, T, D, (81, 82, 83, 84), normal=True)
+    ro, rl = orc.attn_forward(q, k, v, 0.125, causal)
+    rD, rdq, rdk, rdv = orc.attn_backward(q, k, v, ro, do, rl, 0.125, causal)
+
+    def bthd(a):
+        return torch.from_numpy(np.ascontiguousarray(a.transpose(0, 2, 1, 3))).to(DEV).transpose(
+            1, 2)
+
+    def padded(a):
+        buf = torch.full((B, H + 1, T + 5), float("nan"), device=DEV)
+        buf[:, 1:, 2:2 + T] = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+        return buf[:, 1:, 2:2 + T]
+
+    Q, K, V, dO = (bthd(a) for a in (q, k, v, do))
+    L, Dt = padded(rl), padded(rD)
+    assert not Q.is_contiguous() and not L.is_contiguous()
+    dq, dk, dv = (torch.zeros(B, T, H, D, device=DEV).transpose(1, 2) for _ in range(3))
+    hk.attn_backward(Q, K, V, dO, L, Dt, causal, 0.125, dq=dq, dk=dk, dv=dv)
+    torch.cuda.synchronize()
+    rels = [max_rel(g.cpu().numpy(), r) for g, r in ((dq, rdq), (dk, rdk), (dv, rdv))]
+    print(f"dQ {rels[0]:.2e} dK {rels[1]:.2e} dV {rels[2]:.2e}")
+    assert max(rels) <= 2e-3, rels
