@@ -256,7 +256,7 @@ HK_API hipError_t hk_unified_reduce_sum_f32(const hk_reduction_layout* layout, c
  * hk_unified_reduce_sum_f32; the split partials live in a fixed array of
  * HK_REDUCE_NOALLOC_SCRATCH_BYTES that each device holds for the life of the process, instead
  * of the stream's grow-only workspace. The size covers every plan on a 256-CU device (the
- * largest, an outer-axis split, needs 2,096,128 bytes); a plan whose partials need more (split
+ * largest, an outer-axis split, needs 2,095,104 bytes); a plan whose partials need more (split
  * count x num_outputs x 4 bytes, possible on a device with more CUs) returns
  * hipErrorInvalidValue before anything is launched. Calls that overlap on one device share the
  * array: they must be ordered (one stream, or events between streams). */
