@@ -55,20 +55,29 @@ constexpr int BM = 256, BN = 256, BK = 64;             // BN: the full tile widt
 constexpr int kStages = 2;                             // LDS ring depth (k-tiles)
 constexpr int kWaves = 8;                              // 2 x 4 over the tile, 2 per SIMD
 constexpr int kThreads = kWaves * 64;
-constexpr int kWaveM = 128;                            // 4 MFMA tiles of 32 rows per wave
-constexpr int kBlkM = kWaveM / 32;
-constexpr int kStageBytes = 256 * BK * 2;              // the A operand, one k-tile (32 KiB)
-constexpr int kLoadsPerWave = kStageBytes / 1024 / kWaves;  // 16-byte lane copies of A per wave
+
+// Tile height BMT (256, or 192 for products whose 256-row tiles would leave many CUs idle, see
+// row_tile; 192 only with a k-major A): each wave owns BMT / 2 rows of C, kBlkM MFMA tiles of
+// 32 rows.
+template <int BMT>
+struct TileM {
+  static_assert(BMT == 256 || BMT == 192, "tile heights");
+  static constexpr int kWaveM = BMT / 2;
+  static constexpr int kBlkM = kWaveM / 32;
+  static constexpr int kStageBytes = BMT * BK * 2;                   // A, one k-tile
+  static constexpr int kLoadsPerWave = kStageBytes / 1024 / kWaves;  // 16-byte lane copies of A
+};
 
 // Tile width BNT (256, or 128 for the half-width tiles that fill a last round, see
-// column_split): each wave owns 128 x BNT / 4 of C, kBlkN MFMA tiles of 32 columns.
-template <int BNT>
+// column_split): each wave owns BMT / 2 x BNT / 4 of C, kBlkN MFMA tiles of 32 columns.
+template <int BNT, int BMT = 256>
 struct TileN {
   static constexpr int kWaveN = BNT / 4;
   static constexpr int kBlkN = kWaveN / 32;
   static constexpr int kStageBytesB = BNT * BK * 2;
   static constexpr int kLoadsB = kStageBytesB / 1024 / kWaves;
-  static constexpr size_t kLdsBytes = static_cast<size_t>(kStages) * (kStageBytes + kStageBytesB);
+  static constexpr size_t kLdsBytes =
+      static_cast<size_t>(kStages) * (TileM<BMT>::kStageBytes + kStageBytesB);
 };
 
 typedef short bf16x8_t __attribute__((ext_vector_type(8)));
@@ -241,7 +250,7 @@ __device__ __forceinline__ void interleave_reads() {
 // from the MFMA layout instead, every store touched 32 rows and each 128-byte line of C was
 // assembled from 8 stores (bf16): 23% of the BASELINE product. The area is the wave's own, so
 // it needs no barrier beyond the one that ends the main loop.
-template <int kWaveN, typename Out>
+template <int kWaveN, int kBlkM, typename Out>
 __device__ __forceinline__ void staged_rows(const f32x16_t (&acc)[kBlkM][kWaveN / 32],
                                             unsigned char HK_LDS* area, int lane, Out&& out) {
   constexpr int kBlkN = kWaveN / 32;
@@ -323,28 +332,31 @@ struct Bf16RowOut {
 // The operands are swapped in the MFMA (B block as the "A" input), so each lane ends up
 // holding 4 consecutive output columns of one output row per register quad; the epilogue
 // hands them to the output through LDS (staged_rows).
-// One workgroup's tile: tile `wg` of the BM x BNT tiles that cover the columns
+// One workgroup's tile: tile `wg` of the BMT x BNT tiles that cover the columns
 // [n_base, n_end) of C (N bounds the stores).
-template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL, int BNT>
+template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL, int BNT, int BMT = 256>
 __device__ __forceinline__ void tile_body(
     int M, int N, int K, const Epi& ep, const uint16_t* __restrict__ A, int64_t lda, int64_t sA,
     const uint16_t* __restrict__ B, int64_t ldb, int64_t sB, uint16_t* __restrict__ C,
     int64_t ldc, int64_t sC, int split_k, int k_per_split, float* __restrict__ part,
     const hk::F32Out& fo, int n_base, int n_end, int wg) {
+  static_assert(BMT == 256 || A_KMAJOR, "192-row tiles need a k-major A");
   using OA = TileOperand<A_KMAJOR>;
   using OB = TileOperand<B_KMAJOR, BNT>;
-  constexpr int kWaveN = TileN<BNT>::kWaveN, kBlkN = TileN<BNT>::kBlkN;
-  constexpr int kStageBytesB = TileN<BNT>::kStageBytesB, kLoadsB = TileN<BNT>::kLoadsB;
+  constexpr int kWaveN = TileN<BNT, BMT>::kWaveN, kBlkN = TileN<BNT, BMT>::kBlkN;
+  constexpr int kStageBytesB = TileN<BNT, BMT>::kStageBytesB, kLoadsB = TileN<BNT, BMT>::kLoadsB;
+  constexpr int kWaveM = TileM<BMT>::kWaveM, kBlkM = TileM<BMT>::kBlkM;
+  constexpr int kStageBytes = TileM<BMT>::kStageBytes, kLoadsPerWave = TileM<BMT>::kLoadsPerWave;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
   unsigned char HK_LDS* ldsA = (unsigned char HK_LDS*)lds_raw;
   unsigned char HK_LDS* ldsB = ldsA + kStages * kStageBytes;
 
   const int batch = blockIdx.z / split_k;
   const int split = blockIdx.z - batch * split_k;
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (n_end - n_base + BNT - 1) / BNT;
+  const int tiles_m = (M + BMT - 1) / BMT, tiles_n = (n_end - n_base + BNT - 1) / BNT;
   int tm, tn;
   tile_coords(wg, tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = n_base + tn * BNT;
+  const int m0 = tm * BMT, n0 = n_base + tn * BNT;
   const int kbeg = split * k_per_split;
   const int klen = min(K, kbeg + k_per_split) - kbeg;
 
@@ -518,14 +530,14 @@ __device__ __forceinline__ void tile_body(
   // wm*128 + 32 i + l % 32 and columns wn*kWaveN + 32 j + 8 q + 4 (l / 32) .. +3; the rows go
   // out through LDS (staged_rows).
   // every wave is done with the LDS ring: its start becomes the waves' staging areas
-  static_assert(kWaves * 32 * (kWaveN * 4 + 16) <= TileN<BNT>::kLdsBytes, "staging fits");
+  static_assert(kWaves * 32 * (kWaveN * 4 + 16) <= TileN<BNT, BMT>::kLdsBytes, "staging fits");
   __syncthreads();
   unsigned char HK_LDS* area = ldsA + wave * (32 * (kWaveN * 4 + 16));
   const int wrow0 = m0 + wm * kWaveM, wcol0 = n0 + wn * kWaveN;
   if (PARTIAL && fo.C) {
     // one split: fp32 C with alpha, beta and the bias applied here
     float* cb = fo.C + static_cast<int64_t>(batch) * fo.sC;
-    staged_rows<kWaveN>(acc, area, lane, [&](int rr, int cc, const f32x4_t& a, const f32x4_t& b) {
+    staged_rows<kWaveN, kBlkM>(acc, area, lane, [&](int rr, int cc, const f32x4_t& a, const f32x4_t& b) {
       const int row = wrow0 + rr, col = wcol0 + cc;
       if (row >= M || col >= N) return;  // N % 8 == 0
       f32x4_t* dst = reinterpret_cast<f32x4_t*>(cb + static_cast<int64_t>(row) * fo.ldc + col);
@@ -549,7 +561,7 @@ __device__ __forceinline__ void tile_body(
   if (PARTIAL) {
     float* out = part + (static_cast<int64_t>(split) * (gridDim.z / split_k) + batch) *
                             static_cast<int64_t>(M) * N;
-    staged_rows<kWaveN>(acc, area, lane, [&](int rr, int cc, const f32x4_t& a, const f32x4_t& b) {
+    staged_rows<kWaveN, kBlkM>(acc, area, lane, [&](int rr, int cc, const f32x4_t& a, const f32x4_t& b) {
       const int row = wrow0 + rr, col = wcol0 + cc;
       if (row >= M || col >= N) return;
       f32x4_t* dst = reinterpret_cast<f32x4_t*>(out + static_cast<int64_t>(row) * N + col);
@@ -560,21 +572,21 @@ __device__ __forceinline__ void tile_body(
   }
   uint16_t* Cb = C + static_cast<int64_t>(batch) * sC;
   if (ep.bias)
-    staged_rows<kWaveN>(acc, area, lane, Bf16RowOut<true>{ep, Cb, ldc, M, N, wrow0, wcol0});
+    staged_rows<kWaveN, kBlkM>(acc, area, lane, Bf16RowOut<true>{ep, Cb, ldc, M, N, wrow0, wcol0});
   else
-    staged_rows<kWaveN>(acc, area, lane, Bf16RowOut<false>{ep, Cb, ldc, M, N, wrow0, wcol0});
+    staged_rows<kWaveN, kBlkM>(acc, area, lane, Bf16RowOut<false>{ep, Cb, ldc, M, N, wrow0, wcol0});
 }
 
 // One column region: workgroup x takes tile x.
-template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL, int BNT>
+template <bool A_KMAJOR, bool B_KMAJOR, bool PARTIAL, int BNT, int BMT>
 __global__ __launch_bounds__(kThreads, 1) void bgemm_tiled(
     int M, int N, int K, Epi ep, const uint16_t* __restrict__ A, int64_t lda, int64_t sA,
     const uint16_t* __restrict__ B, int64_t ldb, int64_t sB, uint16_t* __restrict__ C,
     int64_t ldc, int64_t sC, int split_k, int k_per_split, float* __restrict__ part,
     hk::F32Out fo, int n_base, int n_end) {
-  tile_body<A_KMAJOR, B_KMAJOR, PARTIAL, BNT>(M, N, K, ep, A, lda, sA, B, ldb, sB, C, ldc, sC,
-                                             split_k, k_per_split, part, fo, n_base, n_end,
-                                             blockIdx.x);
+  tile_body<A_KMAJOR, B_KMAJOR, PARTIAL, BNT, BMT>(M, N, K, ep, A, lda, sA, B, ldb, sB, C, ldc,
+                                                  sC, split_k, k_per_split, part, fo, n_base,
+                                                  n_end, blockIdx.x);
 }
 
 // Both column regions in one launch (column_split): workgroups [0, nfull) take the 256-wide
@@ -678,16 +690,17 @@ float bf16_bits_to_float(hk_bf16 h) {
 
 // BNT 256 or 128: one column region (bgemm_tiled); BNT 0: both regions (bgemm_mixed), with
 // n_base = n_split and n_end = nfull.
-template <bool AK, bool BKM, bool P, int BNT>
+template <bool AK, bool BKM, bool P, int BNT, int BMT = 256>
 hipError_t launch_tiled(dim3 grid, hipStream_t stream, int M, int N, int K, const Epi& ep,
                         const uint16_t* A, int64_t lda, int64_t sA, const uint16_t* B,
                         int64_t ldb, int64_t sB, uint16_t* C, int64_t ldc,
                         int64_t sC, int split_k, int kps, float* part, const hk::F32Out& fo,
                         int n_base, int n_end) {
-  constexpr size_t kLds = TileN<BNT == 0 ? 256 : BNT>::kLdsBytes;
+  static_assert(BNT != 0 || BMT == 256, "the mixed-width launch uses 256-row tiles");
+  constexpr size_t kLds = TileN<BNT == 0 ? 256 : BNT, BMT>::kLdsBytes;
   const void* fn;
   if constexpr (BNT == 0) fn = reinterpret_cast<const void*>(&bgemm_mixed<AK, BKM, P>);
-  else fn = reinterpret_cast<const void*>(&bgemm_tiled<AK, BKM, P, BNT>);
+  else fn = reinterpret_cast<const void*>(&bgemm_tiled<AK, BKM, P, BNT, BMT>);
   static std::once_flag once;
   static hipError_t attr_status = hipSuccess;
   std::call_once(once, [fn] {
@@ -699,13 +712,13 @@ hipError_t launch_tiled(dim3 grid, hipStream_t stream, int M, int N, int K, cons
     hipLaunchKernelGGL((bgemm_mixed<AK, BKM, P>), grid, dim3(kThreads), kLds, stream, M, N, K, ep,
                        A, lda, sA, B, ldb, sB, C, ldc, sC, split_k, kps, part, fo, n_base, n_end);
   else
-    hipLaunchKernelGGL((bgemm_tiled<AK, BKM, P, BNT>), grid, dim3(kThreads), kLds, stream, M, N,
-                       K, ep, A, lda, sA, B, ldb, sB, C, ldc, sC, split_k, kps, part, fo, n_base,
-                       n_end);
+    hipLaunchKernelGGL((bgemm_tiled<AK, BKM, P, BNT, BMT>), grid, dim3(kThreads), kLds, stream, M,
+                       N, K, ep, A, lda, sA, B, ldb, sB, C, ldc, sC, split_k, kps, part, fo,
+                       n_base, n_end);
   return hk::launch_status();
 }
 
-template <bool P, int BNT>
+template <bool P, int BNT, int BMT = 256>
 hipError_t dispatch_layout(bool ta, bool tb, dim3 grid, hipStream_t stream, int M, int N, int K,
                            const Epi& ep, const uint16_t* A, int64_t lda, int64_t sA,
                            const uint16_t* B, int64_t ldb, int64_t sB, uint16_t* C,
@@ -713,16 +726,23 @@ hipError_t dispatch_layout(bool ta, bool tb, dim3 grid, hipStream_t stream, int 
                            const hk::F32Out& fo, int n_base, int n_end) {
   // A is k-major unless transposed; B is k-major only when transposed.
   if (!ta && !tb)
-    return launch_tiled<true, false, P, BNT>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
-                                             C, ldc, sC, split_k, kps, part, fo, n_base, n_end);
+    return launch_tiled<true, false, P, BNT, BMT>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb,
+                                                  sB, C, ldc, sC, split_k, kps, part, fo, n_base,
+                                                  n_end);
   if (!ta && tb)
-    return launch_tiled<true, true, P, BNT>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
-                                            C, ldc, sC, split_k, kps, part, fo, n_base, n_end);
-  if (ta && !tb)
-    return launch_tiled<false, false, P, BNT>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
-                                              C, ldc, sC, split_k, kps, part, fo, n_base, n_end);
-  return launch_tiled<false, true, P, BNT>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
-                                           C, ldc, sC, split_k, kps, part, fo, n_base, n_end);
+    return launch_tiled<true, true, P, BNT, BMT>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb,
+                                                 sB, C, ldc, sC, split_k, kps, part, fo, n_base,
+                                                 n_end);
+  if constexpr (BMT != 256) {
+    return hipErrorInvalidValue;  // row_tile keeps 256-row tiles for an M-major A
+  } else {
+    if (ta && !tb)
+      return launch_tiled<false, false, P, BNT>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb,
+                                                sB, C, ldc, sC, split_k, kps, part, fo, n_base,
+                                                n_end);
+    return launch_tiled<false, true, P, BNT>(grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
+                                             C, ldc, sC, split_k, kps, part, fo, n_base, n_end);
+  }
 }
 
 // Columns [0, n_split) of C take 256 x 256 tiles and [n_split, N) 256 x 128 tiles. One
@@ -752,6 +772,21 @@ int column_split(int M, int N, int work_per_tile) {
   return static_cast<int>((tiles_n - best_c) * BN);
 }
 
+// Rows per tile. 256 x 256 tiles that do not fill one round of the CUs leave the rest idle
+// (8192 x 1280: 160 tiles on 256 CUs). 192-row tiles cut each workgroup's work to 3/4 and
+// raise the tile count (215 there), so they are used when their rounds, each costed 0.75 of a
+// 256-row round, save at least 10%. They need a k-major A (the M-major LDS layout holds 256 or
+// 128 rows) and a single k split.
+int row_tile(bool ta, int M, int N, int grid_z, int split_k) {
+  if (ta || split_k != 1) return 256;
+  const int64_t cus = hk::device_cu_count();
+  const int64_t tiles_n = (N + BN - 1) / BN;
+  const int64_t t256 = static_cast<int64_t>((M + 255) / 256) * tiles_n * grid_z;
+  if (t256 >= cus) return 256;
+  const int64_t t192 = static_cast<int64_t>((M + 191) / 192) * tiles_n * grid_z;
+  return 0.75 * static_cast<double>(hk::ceil_div(t192, cus)) <= 0.9 ? 192 : 256;
+}
+
 // The product over its column regions (column_split), in one launch; grid.z covers batches
 // and splits. A split into partials (P with split_k > 1) keeps one region.
 template <bool P>
@@ -759,6 +794,12 @@ hipError_t run_regions(bool ta, bool tb, int grid_z, hipStream_t stream, int M, 
                        const Epi& ep, const uint16_t* A, int64_t lda, int64_t sA,
                        const uint16_t* B, int64_t ldb, int64_t sB, uint16_t* C, int64_t ldc,
                        int64_t sC, int split_k, int kps, float* part, const hk::F32Out& fo) {
+  if (row_tile(ta, M, N, grid_z, split_k) == 192) {
+    const int64_t tiles = static_cast<int64_t>((M + 191) / 192) * ((N + BN - 1) / BN);
+    const dim3 grid(static_cast<unsigned>(tiles), 1, grid_z);
+    return dispatch_layout<P, 256, 192>(ta, tb, grid, stream, M, N, K, ep, A, lda, sA, B, ldb, sB,
+                                        C, ldc, sC, split_k, kps, part, fo, 0, N);
+  }
   const int64_t tiles_m = (M + BM - 1) / BM;
   const int n_split = split_k == 1 ? column_split(M, N, grid_z) : N;
   const int64_t nfull = tiles_m * ((n_split + BN - 1) / BN);
@@ -953,6 +994,20 @@ extern "C" int hk_bgemm_split_count(int transA, int transB, int M, int N, int K,
                   static_cast<int64_t>(M) * N, true))
     return 1;
   return tiled_splits(M, N, K, batchCount, splitK);
+}
+
+extern "C" int hk_bgemm_tile_rows(int transA, int transB, int M, int N, int K, int batchCount,
+                                  int splitK) {
+  const int splits = hk_bgemm_split_count(transA, transB, M, N, K, batchCount, splitK);
+  if (splits < 0) return -1;
+  if (splits == 0) return 0;
+  const bool ta = transA != 0, tb = transB != 0;
+  const int64_t lda = ta ? M : K, ldb = tb ? K : N;
+  if ((splitK == 0 && (M == 1 || N == 1)) ||
+      !tiled_path(ta, tb, M, N, K, lda, ldb, N, lda * (ta ? K : M), ldb * (tb ? N : K),
+                  static_cast<int64_t>(M) * N, true))
+    return 0;
+  return row_tile(ta, M, N, batchCount * splits, splits);
 }
 
 extern "C" hipError_t hk_bgemm(int transA, int transB, int M, int N, int K, hk_bf16 alpha,

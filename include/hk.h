@@ -319,6 +319,13 @@ HK_API hipError_t hk_bgemm_tn_backward(int M, int N, int K, hk_bf16 alpha, const
                                        long long strideC, int batchCount, hipStream_t stream);
 HK_API int hk_bgemm_split_count(int transA, int transB, int M, int N, int K, int batchCount,
                                 int splitK);
+/* hk_bgemm_tile_rows (no counterpart in the reference: a host-only planning query, like
+ * hk_bgemm_split_count) returns the rows per output tile the MFMA path runs a product of this
+ * shape with: 256, or 192 when 256-row tiles would leave most CUs idle and A is k-major
+ * (transA == 0); 0 for the GEMV and fallback kernels or an empty product, -1 for an invalid
+ * argument. */
+HK_API int hk_bgemm_tile_rows(int transA, int transB, int M, int N, int K, int batchCount,
+                              int splitK);
 
 /* ------------------------------------------------------------------------------------------
  * Batched BF16 GEMV, the M == 1 / N == 1 GEMMs, fp32 accumulation, one bf16 rounding.

@@ -129,8 +129,11 @@ def test_bgemm_backward_baseline_shapes_library_split(hk, orc, which):
     else:
         fn, (M, N, K), (ta, tb) = "hk_bgemm_tn_backward", (1280, 5120, 8192), (1, 0)
     splits = lib.hk_bgemm_split_count(ta, tb, M, N, K, 1, 0)
-    say("bgemm backward baseline", which, "splits", splits)
+    rows = lib.hk_bgemm_tile_rows(ta, tb, M, N, K, 1, 0)
+    say("bgemm backward baseline", which, "splits", splits, "tile rows", rows)
     assert splits == (1 if which == "dA_NT" else 2)
+    # dA's 160 tiles of 256 rows leave 96 CUs idle: it runs on 215 tiles of 192 rows
+    assert rows == (192 if which == "dA_NT" else 256)
     A, B, C0 = _operands(orc, M, N, K, ta, tb, 1000 + M, normal=True)
     first = _run(hk, fn, A, B, C0, M, N, K, ta, tb, 1.0, 0.5)
     second = _run(hk, fn, A, B, C0, M, N, K, ta, tb, 1.0, 0.5)
@@ -141,6 +144,30 @@ def test_bgemm_backward_baseline_shapes_library_split(hk, orc, which):
     rel = max_rel(orc.bf16_to_f32(first[rows]), ref)
     print(f"{which} rel {rel:.2e} over {len(rows)} rows")
     assert rel <= 1e-2
+
+
+@pytest.mark.parametrize("M,N,K", [(192, 256, 64), (200, 264, 136), (400, 512, 72),
+                                   (1000, 136, 520)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1)])
+def test_bgemm_192_row_tiles(hk, orc, M, N, K, ta, tb):
+    # Products with few 256-row tiles and a k-major A run on 192-row tiles: whole and partial
+    # last row tiles, partial column tiles and a K tail, alpha and beta both active
+    lib = hk.lib()
+    assert lib.hk_bgemm_tile_rows(ta, tb, M, N, K, 1, 0) == 192
+    say("bgemm 192-row tiles", M, N, K, ta, tb)
+    A, B, C0 = _operands(orc, M, N, K, ta, tb, 1200 + M)
+    _check(orc, _run(hk, "hk_bgemm", A, B, C0, M, N, K, ta, tb, 1.5, 0.5), A, B, C0, ta, tb, 1.5,
+           0.5)
+
+
+def test_bgemm_tile_rows_query(hk):
+    lib = hk.lib()
+    assert lib.hk_bgemm_tile_rows(0, 0, 8192, 5120, 1280, 1, 0) == 256  # 640 tiles: 2.5 rounds
+    assert lib.hk_bgemm_tile_rows(1, 0, 512, 512, 512, 1, 0) == 256  # M-major A
+    assert lib.hk_bgemm_tile_rows(0, 0, 512, 512, 512, 1, 4) == 256  # split K
+    assert lib.hk_bgemm_tile_rows(0, 0, 1, 512, 512, 1, 0) == 0  # GEMV
+    assert lib.hk_bgemm_tile_rows(0, 0, 0, 512, 512, 1, 0) == 0
+    assert lib.hk_bgemm_tile_rows(0, 0, -1, 512, 512, 1, 0) == -1
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
