@@ -479,10 +479,51 @@ def per_kernel_suite(flush, compute_only=False):
     rdst = torch.empty(16384, device=DEV)
     cases.append(("reduce_inner_16384x50304", lambda: hk.unified_reduce_sum(rs, lay, rdst),
                   16384 * 50304 * 4, "hbm"))
+    cases += step_alone_cases(g)
     cases += gemm_cases(g)
     cases += gemv_cases(g)
     cases += attention_cases(g)
     return time_cases(select(cases), flush, out)
+
+
+def step_alone_cases(g):
+    """The five configs[1] step kernels timed alone like every other memory-bound case (bursts
+    over distinct buffer sets after a cache flush, median of the repetitions), beside their
+    inside-the-step figures: an event pair around each launch inside the step adds a few us,
+    which is a sizeable part of the ~17-25 us GELU kernels."""
+    n = W.numel(W.GELU["shape"])
+    gf, gb = [], []
+    for _ in range(n_sets(W.gelu_bwd_bytes(n, 2))):
+        gx = torch.randn(n, generator=g, device=DEV).to(torch.bfloat16)
+        gg = torch.randn(n, generator=g, device=DEV).to(torch.bfloat16)
+        gy, gi = torch.empty_like(gx), torch.empty_like(gx)
+        gf.append(lambda gx=gx, gy=gy: hk.gelu_forward(gx, gy))
+        gb.append(lambda gg=gg, gx=gx, gi=gi: hk.gelu_backward(gg, gx, gi))
+    R, V = W.CE["rows"], W.CE["vocab"]
+    logits = torch.randn(R, V, generator=g, device=DEV) * 2.0
+    targets = torch.randint(0, V, (R,), generator=g, device=DEV, dtype=torch.int32)
+    loss, mx, sm = (torch.empty(R, device=DEV) for _ in range(3))
+    grad = torch.empty_like(logits)
+    gout = torch.ones(1, device=DEV)
+    hk.sparse_ce_forward(logits, targets, loss, mx, sm)
+    shapes = W.gpt2_param_shapes()
+    P = [torch.randn(W.numel(sh), generator=g, device=DEV) * 0.02 for sh in shapes]
+    G = [torch.randn(W.numel(sh), generator=g, device=DEV) * 1e-2 for sh in shapes]
+    M = [torch.rand(W.numel(sh), generator=g, device=DEV) * 0.1 for sh in shapes]
+    Vv = [torch.rand(W.numel(sh), generator=g, device=DEV) * 0.1 for sh in shapes]
+    plan = hk.AdamPlan(P, G, M, Vv)
+    c = W.ADAMW
+    hyper = (c["lr"], c["beta1"], c["beta2"], c["eps"], c["weight_decay"], 1 - c["beta1"],
+             1 - c["beta2"])
+    return [
+        ("gelu_fwd_bf16_alone", gf, W.gelu_fwd_bytes(n, 2), "hbm"),
+        ("ce_fwd_alone", [lambda: hk.sparse_ce_forward(logits, targets, loss, mx, sm)],
+         W.ce_fwd_bytes(R, V), "hbm"),
+        ("ce_bwd_alone", [lambda: hk.sparse_ce_backward(logits, targets, mx, sm, gout, 1.0, grad)],
+         W.ce_bwd_bytes(R, V), "hbm"),
+        ("gelu_bwd_bf16_alone", gb, W.gelu_bwd_bytes(n, 2), "hbm"),
+        ("adamw_148_alone", [lambda: plan.step(*hyper)], W.adamw_bytes(W.GPT2_NUM_PARAMS), "hbm"),
+    ]
 
 
 def select(cases):
@@ -704,6 +745,10 @@ CEILING_OF = {
     "gelu_fwd_bf16": "ceiling_1r1w_gelu_16bit", "gelu_bwd_bf16": "ceiling_2r1w_gelu_16bit",
     "gelu_fwd_f16": "ceiling_1r1w_gelu_16bit", "gelu_bwd_f16": "ceiling_2r1w_gelu_16bit",
     "ce_fwd": "ceiling_1r0w_ce", "ce_bwd": "ceiling_1r1w_ce", "adamw_148": "ceiling_4r3w_adamw",
+    "gelu_fwd_bf16_alone": "ceiling_1r1w_gelu_16bit",
+    "gelu_bwd_bf16_alone": "ceiling_2r1w_gelu_16bit",
+    "ce_fwd_alone": "ceiling_1r0w_ce", "ce_bwd_alone": "ceiling_1r1w_ce",
+    "adamw_148_alone": "ceiling_4r3w_adamw",
     "reduce_inner_16384x50304": "ceiling_1r0w_1GiB",
 }
 
@@ -839,8 +884,9 @@ def main():
         if ARGS.suite == "all":
             cpu_kernels.update(run_cpu_configs())
             for k, e in cpu_kernels.items():
-                if k in result["per_kernel"]:
-                    result["per_kernel"][k]["cpu"] = e
+                for name in (k, k + "_alone"):
+                    if name in result["per_kernel"]:
+                        result["per_kernel"][name]["cpu"] = e
     print(json.dumps(result), flush=True)
     print_summary(result)
 
@@ -849,8 +895,9 @@ def main():
 SUMMARY = [
     ("configs[0] LayerNorm fp32 4096x768",
      ["ln_fwd", "ln_bwd_fused", "ln_bwd_input", "ln_bwd_gamma_beta"]),
-    ("configs[1] GELU bf16 / CE / AdamW (inside the step)",
-     ["gelu_fwd_bf16", "ce_fwd", "ce_bwd", "gelu_bwd_bf16", "adamw_148"]),
+    ("configs[1] GELU bf16 / CE / AdamW, alone; then inside the step (events per launch)",
+     ["gelu_fwd_bf16_alone", "ce_fwd_alone", "ce_bwd_alone", "gelu_bwd_bf16_alone",
+      "adamw_148_alone", "gelu_fwd_bf16", "ce_fwd", "ce_bwd", "gelu_bwd_bf16", "adamw_148"]),
     ("configs[2] attention fwd 8x12x1024x64",
      ["attn_fwd_causal_8x12x1024x64", "attn_fwd_noncausal_8x12x1024x64"]),
     ("configs[3] attention bwd 8x12x1024x64",
