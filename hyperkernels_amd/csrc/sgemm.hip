@@ -24,7 +24,8 @@
 //     products; roofline the fp32 matrix peak (157.3 TFLOP/s).
 //
 // Design of the fp32 tiles (gfx950): the same tiling as the BF16 GEMM of this library - 256 x 256 workgroup
-// tile, 4 waves of 128 x 128 (4 x 4 MFMA tiles, 256 fp32 accumulators per lane), k-tiles of
+// tile, 8 waves of 128 x 64 (2 x 4, two per SIMD; 4 x 2 MFMA tiles, 128 fp32 accumulators per
+// lane; with 4 waves of 128 x 128 the 256 accumulators spilled), k-tiles of
 // 32 fp32 copied HBM/L2 -> LDS without passing through registers (global_load_lds_dwordx4)
 // into a 2-stage LDS ring, one barrier per k-tile. K-major operands sit in LDS as [row][k]
 // (read 4 k at a time with 16-byte reads), M/N-major ones as [k][row] like in HBM (one float
@@ -44,10 +45,12 @@ namespace {
 
 constexpr int BM = 256, BN = 256, BK = 32;
 constexpr int kStages = 2;                             // LDS ring depth (k-tiles)
-constexpr int kThreads = 256;
-constexpr int kWave = 128;
+constexpr int kWaves = 8;                              // 2 x 4 over the tile, 2 per SIMD
+constexpr int kThreads = kWaves * 64;
+constexpr int kWaveM = 128, kWaveN = 64;               // 4 x 2 MFMA tiles of 32 x 32 per wave
+constexpr int kBlkM = kWaveM / 32, kBlkN = kWaveN / 32;
 constexpr int kStageBytes = 256 * BK * 4;              // one operand, one k-tile (32 KiB)
-constexpr int kLoadsPerWave = kStageBytes / 1024 / 4;  // 16-byte lane copies per operand per wave
+constexpr int kLoadsPerWave = kStageBytes / 1024 / kWaves;  // 16-byte lane copies per operand per wave
 constexpr size_t kLdsBytes = static_cast<size_t>(kStages) * 2 * kStageBytes;  // 128 KiB
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -148,21 +151,21 @@ __device__ __forceinline__ float bias_at(const Epilogue& ep, int M, int N, int b
 
 __device__ __forceinline__ float f4_get(const f32x4_t& v, int e) { return v[e]; }
 
-// 16 MFMAs (4 x 4 blocks) of one k step; B block as the MFMA "A" input so that each lane ends
-// up holding 4 consecutive output columns of one output row per accumulator quad.
-__device__ __forceinline__ void mma_quad(const f32x4_t (&af)[4], const f32x4_t (&bf)[4],
-                                         f32x16_t (&acc)[4][4]) {
+// 8 MFMAs (4 x 2 blocks) per k step, 4 k steps; B block as the MFMA "A" input so that each
+// lane ends up holding 4 consecutive output columns of one output row per accumulator quad.
+__device__ __forceinline__ void mma_quad(const f32x4_t (&af)[kBlkM], const f32x4_t (&bf)[kBlkN],
+                                         f32x16_t (&acc)[kBlkM][kBlkN]) {
 #pragma unroll
   for (int e = 0; e < 4; ++e)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kBlkM; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < kBlkN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4_get(bf[j], e), f4_get(af[i], e),
                                                          acc[i][j], 0, 0, 0);
 }
 
-// Main loop per k-tile kt (ring slot kt % 2) in 4 quads of 4 MFMA steps (64 MFMAs each):
+// Main loop per k-tile kt (ring slot kt % 2) in 4 quads of 4 MFMA steps (32 MFMAs each):
 // quads 0-2 read the operands of the next quad while multiplying; quad 3 waits for this
 // wave's copies of tile kt + 1, takes the barrier, reads quad 0 of tile kt + 1 and issues the
 // copies of tile kt + 2 into slot kt % 2 between its MFMAs.
@@ -188,7 +191,7 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_tiled(
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
 
   // Rows past M (N) are read clamped (their outputs are not stored); k past the split's end is
   // zero-filled on the last k-tile.
@@ -236,11 +239,11 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_tiled(
   };
   constexpr int kCopies = 2 * kLoadsPerWave;
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[kBlkM][kBlkN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kBlkM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+    for (int j = 0; j < kBlkN; ++j) acc[i][j] = f32x16_t{};
 
 #pragma unroll
   for (int p = 0; p < kStages; ++p)
@@ -252,12 +255,12 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_tiled(
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
 
-  f32x4_t fa[2][4], fb[2][4];
+  f32x4_t fa[2][kBlkM], fb[2][kBlkN];
   if (ktiles > 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[0][i] = OA::read(ldsA, wm * kWave, i, 0, lane);
+    for (int i = 0; i < kBlkM; ++i) fa[0][i] = OA::read(ldsA, wm * kWaveM, i, 0, lane);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) fb[0][j] = OB::read(ldsB, wn * kWave, j, 0, lane);
+    for (int j = 0; j < kBlkN; ++j) fb[0][j] = OB::read(ldsB, wn * kWaveN, j, 0, lane);
   }
 
   for (int kt = 0; kt < ktiles; ++kt) {
@@ -269,9 +272,9 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_tiled(
       const int cur = qd & 1, nxt = cur ^ 1;
       if (qd + 1 < 4) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) fa[nxt][i] = OA::read(sa, wm * kWave, i, qd + 1, lane);
+        for (int i = 0; i < kBlkM; ++i) fa[nxt][i] = OA::read(sa, wm * kWaveM, i, qd + 1, lane);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) fb[nxt][j] = OB::read(sb, wn * kWave, j, qd + 1, lane);
+        for (int j = 0; j < kBlkN; ++j) fb[nxt][j] = OB::read(sb, wn * kWaveN, j, qd + 1, lane);
         mma_quad(fa[cur], fb[cur], acc);
       } else {
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
@@ -280,22 +283,22 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_tiled(
           const unsigned char HK_LDS* na = ldsA + (slot ^ 1) * kStageBytes;
           const unsigned char HK_LDS* nb = ldsB + (slot ^ 1) * kStageBytes;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) fa[nxt][i] = OA::read(na, wm * kWave, i, 0, lane);
+          for (int i = 0; i < kBlkM; ++i) fa[nxt][i] = OA::read(na, wm * kWaveM, i, 0, lane);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) fb[nxt][j] = OB::read(nb, wn * kWave, j, 0, lane);
+          for (int j = 0; j < kBlkN; ++j) fb[nxt][j] = OB::read(nb, wn * kWaveN, j, 0, lane);
         }
         const bool more = kt + kStages < ktiles;
         const bool fill = tail && kt + kStages == ktiles - 1;
-        // 64 MFMAs with the 16 copies of tile kt + 2 spread between them
+        // 32 MFMAs with the 8 copies of tile kt + 2 spread between them
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < kBlkM; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < kBlkN; ++j) {
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
                   f4_get(fb[cur][j], e), f4_get(fa[cur][i], e), acc[i][j], 0, 0, 0);
-              const int q = (e * 16 + i * 4 + j);
+              const int q = (e * kBlkM + i) * kBlkN + j;
               if (more && (q & 3) == 0 && (q >> 2) < kCopies) copy(kt + kStages, slot, q >> 2, fill);
             }
       }
@@ -303,18 +306,18 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_tiled(
   }
 
   // Epilogue. Lane l holds, for MFMA block (i, j) and quad q, output row
-  // wm*128 + 32 i + l % 32 and columns wn*128 + 32 j + 8 q + 4 (l / 32) .. +3.
-  const int row0 = m0 + wm * kWave + (lane & 31);
-  const int col0 = n0 + wn * kWave + 4 * (lane >> 5);
+  // wm*128 + 32 i + l % 32 and columns wn*64 + 32 j + 8 q + 4 (l / 32) .. +3.
+  const int row0 = m0 + wm * kWaveM + (lane & 31);
+  const int col0 = n0 + wn * kWaveN + 4 * (lane >> 5);
   if (PARTIAL) {
     float* out = part + (static_cast<int64_t>(split) * (gridDim.z / split_k) + batch) *
                             static_cast<int64_t>(M) * N;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kBlkM; ++i) {
       const int row = row0 + 32 * i;
       if (row >= M) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < kBlkN; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int col = col0 + 32 * j + 8 * q;
@@ -328,12 +331,12 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_tiled(
   }
   float* Cb = C + static_cast<int64_t>(batch) * sC;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kBlkM; ++i) {
     const int row = row0 + 32 * i;
     if (row >= M) continue;
     float* crow = Cb + static_cast<int64_t>(row) * ldc;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < kBlkN; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int col = col0 + 32 * j + 8 * q;

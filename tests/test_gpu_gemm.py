@@ -470,7 +470,10 @@ def test_sgemm_tile_kernel_entry_point(hk, orc, lay):
 
 
 @pytest.mark.parametrize("M,N,K,lay", [(260, 264, 100, "NN"), (260, 264, 100, "NT"),
-                                       (260, 264, 100, "TN"), (300, 256, 64, "TN")])
+                                       (260, 264, 100, "TN"), (300, 256, 64, "TN"),
+                                       # whole 256 x 256 tiles, 16 k-tiles with a K tail
+                                       (768, 512, 516, "NN"), (768, 512, 516, "NT"),
+                                       (516, 512, 768, "TN")])
 @pytest.mark.parametrize("split_k", [1, 2])
 def test_sgemm_fp32_tile_path(hk, orc, M, N, K, lay, split_k):
     # K (or M for TN) a multiple of 4 but not of 8: the fp32 MFMA tiles, not the bf16x3 path
