@@ -419,12 +419,16 @@ def test_sgemm_bias_strides_and_batches(hk, orc):
 
 
 @pytest.mark.parametrize("lay", ["NN", "TN"])
-def test_sgemm_one_split_writes_c_from_the_tiles(hk, orc, lay):
-    # 4 batches of 2048 x 2048 fill the device with 256 output tiles, so the bf16x3 path runs
-    # with one k split and the GEMM tiles apply alpha, beta and the bias to C themselves
+@pytest.mark.parametrize("split_k", [1, 3])
+def test_sgemm_tiles_write_c_one_split_or_serial_ranges(hk, orc, lay, split_k):
+    # 4 batches of 2048 x 2048 fill the device with 256 output tiles, so the GEMM tiles apply
+    # alpha, beta and the bias to C themselves: with one k split, or with 3 (3 K = 768, 12
+    # k-tiles, 3 ranges of 4) added into C one after the other, beta and the bias in the first
+    # only. A bias added per range would be off by 2 bias, beta applied per range by a power.
     M, N, K, batch = 2048, 2048, 256, 4
     enum, ta, tb = SG_LAYOUT[lay]
-    say("sgemm one split", lay)
+    say("sgemm tiles write C", lay, "split_k", split_k)
+    assert hk.lib().hk_sgemm_split_count(enum, M, N, K, batch, split_k) == split_k
     As = [_sg_operands(orc, M, N, K, ta, tb, 300 + 10 * b) for b in range(batch)]
     A = torch.from_numpy(np.stack([x[0] for x in As])).to(DEV)
     B = torch.from_numpy(np.stack([x[1] for x in As])).to(DEV)
@@ -434,7 +438,8 @@ def test_sgemm_one_split_writes_c_from_the_tiles(hk, orc, lay):
         C = torch.from_numpy(C0.copy()).to(DEV)
         out = _sg_call(hk, "hk_sgemm", enum, A, B, C, M, N, K, 1.5, -0.5,
                        bias=torch.from_numpy(np.ascontiguousarray(bias_np)).to(DEV),
-                       bias_stride=stride, batch=batch, sA=M * K, sB=K * N, sC=M * N)
+                       bias_stride=stride, batch=batch, sA=M * K, sB=K * N, sC=M * N,
+                       split_k=split_k)
         for b in range(batch):
             ref = orc.sgemm(ta, tb, As[b][0], As[b][1], alpha=1.5, beta=-0.5, C0=C0[b])
             if stride == N:
@@ -501,8 +506,9 @@ def test_sgemm_ragged(hk, orc, M, N, K, lay):
 @pytest.mark.parametrize("lay", ["NN", "NT", "TN"])
 @pytest.mark.parametrize("split_k", [4, 0])
 def test_sgemm_baseline_shape_split_k4_sampled_rows(hk, orc, lay, split_k):
-    # 4096^3 with split-K 4 (4 k splits really run: fp32 partials summed
-    # in split order by the finalize) and the fused bias; split_k 0 is the library's own plan.
+    # 4096^3 with split-K 4 (4 k ranges really run: the 256 output tiles
+    # fill the device, so the ranges are added into C in split order) and the fused bias;
+    # split_k 0 is the library's own plan.
     # beta = 1 with C0 ~ N(0, 1) and the bias ~ N(0, 0.02) against a product of std 1/64: a
     # bias added once per split (the reference's split-K epilogue) would be off by 3 * bias,
     # ~8x the 2e-3 bound, and beta * C applied per split by 3 * C0. 64 rows checked in full.
