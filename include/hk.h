@@ -391,8 +391,10 @@ HK_API hipError_t hk_bgemm_core_bias(int layout, int splitK, int M, int N, int K
  *   bias_stride selects it as in the reference (:303-315): N -> bias[col];
  *   M*N -> bias[(batch % M) * N + col]; 1 -> bias[0]; any other value is rejected.
  *   splitK >= 1 cuts the k loop into splitK ranges as the reference does (k_chunk rounded to
- *   the k-tile, :123-126; on the bf16x3 path the tripled k axis) whose fp32 partials are summed
- *   in split order; splitK = 0 lets the library choose. The reference's split-K pre-scale
+ *   the k-tile, :123-126; on the bf16x3 path the tripled k axis) whose products are summed in
+ *   split order: as fp32 partials with a finishing pass, or, when the output tiles alone fill
+ *   the device, added into C range after range (beta and the bias with the first); splitK = 0
+ *   lets the library choose. Calls that overlap on one C race. The reference's split-K pre-scale
  *   kernel sgemm_sm89_scale_kernel (:329-333) is folded in: no caller pre-pass is needed.
  * hk_sgemm_addmm replaces sgemm_addmm_sm89_kernel (blas/fp32/sgemm_addmm_sm89_kernel.cu:66-76):
  *   NN, C = alpha * A B + beta * C + beta * bias, bias_numel in {1, N, M*N} as there.
