@@ -13,10 +13,10 @@
 //   - hk_multi_tensor_adam: the reference's by-value launch metadata (<= 48 tensors,
 //     <= 320 chunks of 32768 elements per launch).
 //   - the plan API: the tensor table and chunk table of any number of tensors live in device
-//     memory, built once, so a whole-model step (GPT-2 small: 148 tensors, 30,450 chunks of
-//     4096 elements) is a single launch with no host-to-device traffic.
+//     memory, built once, so a whole-model step (GPT-2 small: 148 tensors, 243,090 chunks of
+//     512 elements) is a single launch with no host-to-device traffic.
 // Each workgroup streams one chunk: a scalar head up to the first 16-byte boundary, 16-byte
-// loads of p, g, m, v in the body (four vectors of each in flight per lane), and a scalar
+// loads of p, g, m, v in the body (2 or 4 vectors of each in flight per lane), and a scalar
 // tail. Every body load and store is non-temporal: each byte is touched exactly once, and
 // streaming all seven arrays past the caches measured ~10% faster on MI355X than cached
 // accesses for this 4-read / 3-write mix. A tensor whose four arrays do not share the same 16-byte phase is processed scalar.
@@ -27,11 +27,16 @@
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
-// Elements per workgroup in the plan's chunk table: one pass of kUnroll 16-byte vectors per
-// lane, so each workgroup is short-lived and the device keeps many of them in flight.
-constexpr int kPlanChunk = kThreads * kUnroll * 4;
+// Workgroup shapes (lanes, 16-byte vectors of each array per lane per pass). The reference
+// metadata front end streams 32768-element chunks with 256 lanes x 4 vectors. The plan front
+// end gives each one-wave workgroup a single pass of 64 lanes x 2 vectors: 512 elements, so
+// workgroups are short-lived and many are in flight (GPT-2 small's step, same run: 599.5 us
+// at 256 x 4, 581.9 us at 64 x 2; 64 x 3 / 64 x 4 / 128 x 2 / 256 x 2 measured 585-590 us,
+// 1 vector per lane 619-661 us).
+constexpr int kMetaThreads = 256, kMetaUnroll = 4;
+constexpr int kPlanThreads = 64, kPlanUnroll = 2;
+// Elements per workgroup in the plan's chunk table.
+constexpr int kPlanChunk = kPlanThreads * kPlanUnroll * 4;
 
 struct AdamHyper {
   float lr, beta1, beta2, eps, wd, bc1, bc2;
@@ -61,7 +66,8 @@ __device__ __forceinline__ int phase16(const float* p) {
   return static_cast<int>((reinterpret_cast<uintptr_t>(p) >> 2) & 3);
 }
 
-// Updates elements [start, end) of one tensor.
+// Updates elements [start, end) of one tensor with a workgroup of THREADS lanes.
+template <int THREADS, int UNROLL>
 __device__ __forceinline__ void adam_chunk(float* __restrict__ p, const float* __restrict__ g,
                                            float* __restrict__ m, float* __restrict__ v,
                                            int64_t start, int64_t end, const AdamHyper& h) {
@@ -75,7 +81,7 @@ __device__ __forceinline__ void adam_chunk(float* __restrict__ p, const float* _
   }
   // scalar head [start, vs) and, when not vectorised, the whole range
   const int64_t head_end = vec ? vs : end;
-  for (int64_t i = start + threadIdx.x; i < head_end; i += kThreads) {
+  for (int64_t i = start + threadIdx.x; i < head_end; i += THREADS) {
     float pi = p[i], mi = m[i], vi = v[i];
     adam_update(pi, g[i], mi, vi, h);
     p[i] = pi; m[i] = mi; v[i] = vi;
@@ -86,12 +92,12 @@ __device__ __forceinline__ void adam_chunk(float* __restrict__ p, const float* _
   float4* m4 = reinterpret_cast<float4*>(m + vs);
   float4* v4 = reinterpret_cast<float4*>(v + vs);
   const int64_t nv = (ve - vs) >> 2;
-  // kUnroll vectors of each of p, g, m, v per lane per pass, all loads issued before any math
-  for (int64_t i = threadIdx.x; i < nv; i += kUnroll * kThreads) {
-    float4 pa[kUnroll], ga[kUnroll], ma[kUnroll], va[kUnroll];
+  // UNROLL vectors of each of p, g, m, v per lane per pass, all loads issued before any math
+  for (int64_t i = threadIdx.x; i < nv; i += UNROLL * THREADS) {
+    float4 pa[UNROLL], ga[UNROLL], ma[UNROLL], va[UNROLL];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t k = i + u * kThreads;
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t k = i + u * THREADS;
       if (k < nv) {
         pa[u] = hk::ld_nt(p4 + k);
         ga[u] = hk::ld_nt(g4 + k);
@@ -100,8 +106,8 @@ __device__ __forceinline__ void adam_chunk(float* __restrict__ p, const float* _
       }
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t k = i + u * kThreads;
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t k = i + u * THREADS;
       if (k < nv) {
         adam_update4(pa[u], ga[u], ma[u], va[u], h);
         hk::st_nt(p4 + k, pa[u]);
@@ -110,7 +116,7 @@ __device__ __forceinline__ void adam_chunk(float* __restrict__ p, const float* _
       }
     }
   }
-  for (int64_t j = ve + threadIdx.x; j < end; j += kThreads) {
+  for (int64_t j = ve + threadIdx.x; j < end; j += THREADS) {
     float pj = p[j], mj = m[j], vj = v[j];
     adam_update(pj, g[j], mj, vj, h);
     p[j] = pj; m[j] = mj; v[j] = vj;
@@ -118,7 +124,7 @@ __device__ __forceinline__ void adam_chunk(float* __restrict__ p, const float* _
 }
 
 // ---- reference metadata front end -------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void adam_meta_kernel(hk_adam_launch_metadata meta,
+__global__ __launch_bounds__(kMetaThreads) void adam_meta_kernel(hk_adam_launch_metadata meta,
                                                              AdamHyper h) {
   const int b = blockIdx.x;
   if (b >= HK_ADAM_MAX_BLOCKS) return;
@@ -128,7 +134,8 @@ __global__ __launch_bounds__(kThreads) void adam_meta_kernel(hk_adam_launch_meta
   int64_t end = start + HK_ADAM_CHUNK_SIZE;
   if (end > numel) end = numel;
   if (start >= end) return;
-  adam_chunk(meta.params[t], meta.grads[t], meta.ms[t], meta.vs[t], start, end, h);
+  adam_chunk<kMetaThreads, kMetaUnroll>(meta.params[t], meta.grads[t], meta.ms[t], meta.vs[t],
+                                        start, end, h);
 }
 
 // ---- plan front end ------------------------------------------------------------------------
@@ -144,7 +151,7 @@ struct ChunkEntry {
   int32_t chunk;
 };
 
-__global__ __launch_bounds__(kThreads) void adam_plan_kernel(const TensorEntry* __restrict__ tensors,
+__global__ __launch_bounds__(kPlanThreads) void adam_plan_kernel(const TensorEntry* __restrict__ tensors,
                                                              const ChunkEntry* __restrict__ chunks,
                                                              AdamHyper h) {
   const ChunkEntry c = chunks[blockIdx.x];
@@ -153,7 +160,7 @@ __global__ __launch_bounds__(kThreads) void adam_plan_kernel(const TensorEntry* 
   int64_t end = start + kPlanChunk;
   if (end > t.numel) end = t.numel;
   if (start >= end) return;
-  adam_chunk(t.p, t.g, t.m, t.v, start, end, h);
+  adam_chunk<kPlanThreads, kPlanUnroll>(t.p, t.g, t.m, t.v, start, end, h);
 }
 
 }  // namespace
@@ -174,7 +181,8 @@ extern "C" hipError_t hk_multi_tensor_adam(const hk_adam_launch_metadata* meta, 
   if (num_blocks == 0) return hipSuccess;
   for (int b = 0; b < num_blocks; ++b) HK_CHECK_ARG(meta->block_to_tensor[b] < HK_ADAM_MAX_TENSORS);
   const AdamHyper h{lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2};
-  hipLaunchKernelGGL(adam_meta_kernel, dim3(num_blocks), dim3(kThreads), 0, stream, *meta, h);
+  hipLaunchKernelGGL(adam_meta_kernel, dim3(num_blocks), dim3(kMetaThreads), 0, stream, *meta,
+                     h);
   return hk::launch_status();
 }
 
@@ -226,7 +234,7 @@ extern "C" hipError_t hk_adam_plan_step(const hk_adam_plan* plan, float lr, floa
   if (plan->num_chunks == 0) return hipSuccess;
   const AdamHyper h{lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2};
   hipLaunchKernelGGL(adam_plan_kernel, dim3(static_cast<unsigned>(plan->num_chunks)),
-                     dim3(kThreads), 0, stream, plan->d_tensors, plan->d_chunks, h);
+                     dim3(kPlanThreads), 0, stream, plan->d_tensors, plan->d_chunks, h);
   return hk::launch_status();
 }
 
