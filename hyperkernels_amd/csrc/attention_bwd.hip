@@ -27,10 +27,10 @@
 // MFMAs are issued one at a time with the P / dS work that does not depend on them in between,
 // so each wave overlaps its own VALU and matrix work (measured 2-3% faster than issuing each
 // product's MFMAs together after the VALU work it needs). dS^T goes through
-// LDS once so that dQ = dS K is formed per (query block, d block, key half) with lanes along the
-// head dimension; the two key halves are summed through LDS and each dQ element receives one
-// atomic add per key tile. The two query halves' dK / dV partials are summed through LDS at the
-// end. 128-key tiles mean 8 dQ passes per query row at T = 1024 (the reference's 16-key tiles
+// LDS once, and dQ = dS K is formed on 16 x 16 x 32 MFMA blocks, each wave owning 16 queries x
+// 32 d over all 128 keys of the tile, so each dQ element receives one atomic add per key tile
+// with no exchange between waves. The two query halves' dK / dV partials are summed through LDS
+// at the end. 128-key tiles mean 8 dQ passes per query row at T = 1024 (the reference's 16-key tiles
 // make 64). Workgroups are ordered key tile major, so under causal masking the longest ones are
 // dispatched first.
 #include <mutex>
@@ -58,8 +58,7 @@ constexpr int kOffOh = kOffQl + kQPlane, kOffOl = kOffOh + kQPlane;  // dO
 constexpr int kOffSh = kOffOl + kQPlane, kOffSl = kOffSh + kKPlane;  // dS^T [key][query]
 constexpr int kOffL = kOffSl + kKPlane;
 constexpr int kOffD = kOffL + kBQ * 4;
-constexpr int kOffPark = kOffD + kBQ * 4;      // dQ key-half exchange: 4 x 32 x 33 floats
-constexpr size_t kLdsBytes = kOffPark + 4 * 32 * 33 * 4;  // 148,480 bytes
+constexpr size_t kLdsBytes = kOffD + kBQ * 4;  // 131,584 bytes
 // The final dK / dV exchange reuses the start of LDS (4 key groups x 2 x 32 x 65 floats).
 static_assert(4 * 2 * 32 * 65 * 4 <= kLdsBytes, "dK / dV exchange fits");
 static_assert(kLdsBytes <= 160 * 1024, "fits gfx950's 160 KiB of LDS");
@@ -104,6 +103,9 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_
 // v_mfma_f32_32x32x16_bf16: A (32 x 16) lane l holds row l % 32, k = 8 (l / 32) .. + 7; B (16 x 32)
 // lane l holds column l % 32, same k; C element i of lane l is (row 8 (i / 4) + 4 (l / 32) + i % 4,
 // column l % 32).
+// v_mfma_f32_16x16x32_bf16 (dQ): A (16 x 32) lane l holds row l % 16 and B (32 x 16) column
+// l % 16, each with 8 k values of lane group l / 16 (the pairing of A and B values is all the
+// sum over k needs); C element r of lane l is (row 4 (l / 16) + r, column l % 16).
 __device__ __forceinline__ f32x16_t mfma3(bf16x8_t ah, bf16x8_t al, bf16x8_t bh, bf16x8_t bl,
                                           f32x16_t c) {
   c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, c, 0, 0, 0);
@@ -324,12 +326,21 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
     tva[db] = (4 * hh + jj) * kRowBytes + (((4 * db + x) ^ (sbit | hh)) << 4) + colb;
     tvb[db] = (4 * hh + 8 + jj) * kRowBytes + (((4 * db + x) ^ (sbit | ((hh + 2) & 3))) << 4) + colb;
   }
-  // dQ: rows 64 kh + 16 ks + 8 hh + {0..3} and + 4; dS^T columns 32 qb + ..., K columns 32 db + ...
-  const int qb = (wave >> 1) & 1, dbq = wave & 1, kh = wave >> 2;
-  const int tsa = (8 * hh + jj) * kRowBytes + (((4 * qb + x) ^ (sbit | (2 * hh))) << 4) + colb;
-  const int tsb = (8 * hh + 4 + jj) * kRowBytes + (((4 * qb + x) ^ (sbit | (2 * hh + 1))) << 4) + colb;
-  const int tka = (8 * hh + jj) * kRowBytes + (((4 * dbq + x) ^ (sbit | (2 * hh))) << 4) + colb;
-  const int tkb = (8 * hh + 4 + jj) * kRowBytes + (((4 * dbq + x) ^ (sbit | (2 * hh + 1))) << 4) + colb;
+  // dQ on 16 x 16 x 32 MFMA blocks: wave w owns queries 16 (w / 2) .. + 15 and d 32 (w % 2) .. + 31
+  // (two 16 x 16 blocks sharing the dS operand) over all 128 keys, so no exchange between
+  // waves is needed. Both operands are read transposed (contraction over their rows = keys):
+  // lane group g = lane / 16 takes keys 32 ks + 8 g .. + 7 of its column, as two 4-row reads.
+  const int qb16 = wave >> 1, dh = wave & 1;
+  const int g16 = lane >> 4, c4 = (j15 & 3) >> 1, cb8 = 8 * (j15 & 1);
+  const int s16a = sbit | (2 * (g16 & 1)), s16b = sbit | (2 * (g16 & 1) + 1);
+  const int tsa = (8 * g16 + jj) * kRowBytes + (((2 * qb16 + c4) ^ s16a) << 4) + cb8;
+  const int tsb = (8 * g16 + 4 + jj) * kRowBytes + (((2 * qb16 + c4) ^ s16b) << 4) + cb8;
+  int tka[2], tkb[2];
+#pragma unroll
+  for (int jb = 0; jb < 2; ++jb) {
+    tka[jb] = (8 * g16 + jj) * kRowBytes + (((4 * dh + 2 * jb + c4) ^ s16a) << 4) + cb8;
+    tkb[jb] = (8 * g16 + 4 + jj) * kRowBytes + (((4 * dh + 2 * jb + c4) ^ s16b) << 4) + cb8;
+  }
   // dS^T writes: row 32 kg + c, queries 32 qh + 8 g + 4 hh .. + 3
   int wsd[4];
 #pragma unroll
@@ -511,51 +522,38 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(hk_attn_bwd_param
     // every wave is done with this tile's Q / dO / LSE / D: the next tile's copies land while
     // the dQ phase runs
     if (it + 1 < nq) copy_tile(tile_q(it + 1));
-    // dQ block (queries 32 qb.., d 32 dbq..), key half kh of this wave = dS[q][keys] K[keys][d]:
-    // both operands are read transposed (contraction over their rows = keys).
-    f32x16_t dq = f32x16_t{};
+    // dQ (queries 16 qb16 .., d 32 dh + 16 jb ..) = dS[q][keys] K[keys][d] over the 128 keys
+    f32x4_t dq[2] = {f32x4_t{}, f32x4_t{}};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const int rb = (64 * kh + 16 * ks) * kRowBytes;
-      dq = mfma3(rdtr(sSh + rb, tsa, tsb), rdtr(sSl + rb, tsa, tsb), rdtr(sKh + rb, tka, tkb),
-                 rdtr(sKl + rb, tka, tkb), dq);
+      const int rb = 32 * ks * kRowBytes;
+      const bf16x8_t ah = rdtr(sSh + rb, tsa, tsb), al = rdtr(sSl + rb, tsa, tsb);
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        const bf16x8_t bh = rdtr(sKh + rb, tka[jb], tkb[jb]), bl = rdtr(sKl + rb, tka[jb], tkb[jb]);
+        dq[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, dq[jb], 0, 0, 0);
+        dq[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, dq[jb], 0, 0, 0);
+        dq[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, dq[jb], 0, 0, 0);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
-    // dq layout: query 32 qb + 8 (i/4) + 4 hh + i%4, d 32 dbq + c. The two key halves of a
-    // block split its rows: key half h finishes registers i in [8 h, 8 h + 8) (rows 0 .. 15 or
-    // 16 .. 31 of the block) and parks the other 8 in the exchange area for its partner; each
-    // adds the partner's parked values to its own and issues 8 atomics. The area is read before
-    // the barrier at the top of the next query tile, so the next tile's parking cannot race it.
-    float HK_LDS* park = (float HK_LDS*)(lds + kOffPark) + (wave & 3) * (32 * 33);
-    float HK_LDS* pbase = park + 4 * hh * 33 + c;
-    auto row_of = [](int i) { return 8 * (i >> 2) + (i & 3); };
-    if (kh == 0) {
-#pragma unroll
-      for (int i = 8; i < 16; ++i) pbase[row_of(i) * 33] = dq[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) pbase[row_of(i) * 33] = dq[i];
-    }
-    __syncthreads();
     {
-      // wave-uniform row base plus a 32-bit per-lane offset (row 4 hh, column c); the
-      // per-register row steps (8 (i/4) + i%4) * stride are uniform too. Every lane issues
-      // exactly kAtomicsPerTile atomics (the count the next tile's vmcnt wait assumes): a row
-      // past T adds 0 to row T - 1 instead.
-      const int64_t qblk = q0 + 32 * qb;
-      float* dqu = dQb + qblk * p.dq_strideM + 32 * dbq;
-      const int loff = static_cast<int>(4 * hh * p.dq_strideM) + c;
-      const int rows_left = T - qblk < 32 ? static_cast<int>(T - qblk) : 32;  // rows < T
+      // dq[jb][r]: query 16 qb16 + 4 g16 + r, d 32 dh + 16 jb + j15. Every lane issues exactly
+      // kAtomicsPerTile atomics (the count the next tile's vmcnt wait assumes): a row past T
+      // adds 0 to row T - 1 instead.
+      const int64_t qblk = q0 + 16 * qb16 + 4 * g16;
+      const int rows_left = T - qblk < 4 ? static_cast<int>(T - qblk) : 4;  // may be <= 0
+      float* dqu = dQb + qblk * p.dq_strideM + 32 * dh + j15;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        if ((i >> 3) != kh) continue;  // wave-uniform
-        const int rs = row_of(i);
-        const bool in = 4 * hh + rs < rows_left;
-        const float v = in ? (dq[i] + pbase[rs * 33]) * p.scale : 0.f;
-        float* dst = in ? dqu + rs * p.dq_strideM + loff
-                        : dQb + (T - 1) * p.dq_strideM + 32 * dbq + c;
-        unsafeAtomicAdd(dst, v);
-      }
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool in = r < rows_left;
+          const float v = in ? dq[jb][r] * p.scale : 0.f;
+          float* dst = in ? dqu + r * p.dq_strideM + 16 * jb
+                          : dQb + (T - 1) * p.dq_strideM + 32 * dh + 16 * jb + j15;
+          unsafeAtomicAdd(dst, v);
+        }
     }
   }
 
