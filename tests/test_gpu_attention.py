@@ -131,7 +131,9 @@ def test_attn_backward_gpu_chain(hk, orc, causal):
     _bwd_check(hk, orc, q, k, v, do, causal, 0.125, from_gpu_forward=True)
 
 
-@pytest.mark.parametrize("T", [1, 33, 100, 129, 300])
+# 63 / 65 / 127 / 191 / 257: query tiles that end inside a 16-query dQ block or a 4-row group
+# of it (rows past T add 0 to row T - 1)
+@pytest.mark.parametrize("T", [1, 33, 63, 65, 100, 127, 129, 191, 257, 300])
 @pytest.mark.parametrize("causal", [False, True])
 def test_attn_backward_ragged_T(hk, orc, T, causal):
     say("attn bwd ragged", T, causal)
