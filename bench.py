@@ -64,7 +64,7 @@ def _args():
 ARGS = _args()
 if ARGS.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
     print("bench.py: this build measures one GPU only (every kernel runs on one MI355X; "
-          "see DESIGN.md for how the surface would shard). Run with --gpus 1.", file=sys.stderr)
+          "sharding across GPUs is not built). Run with --gpus 1.", file=sys.stderr)
     sys.exit(2)
 
 import torch  # noqa: E402
