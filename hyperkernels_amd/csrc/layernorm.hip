@@ -19,6 +19,7 @@
 // workgroups in a fixed order by a second small kernel: the result is deterministic, unlike
 // the reference's atomics. Shapes outside the register path use a workgroup-per-row fallback.
 #include <initializer_list>
+#include <mutex>
 #include <type_traits>
 
 #include "hk_device.h"
@@ -112,19 +113,33 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_reg(const uint4* __restrict__
 // per CU (8 waves) or two (4 waves), so each CU holds 8 waves and writes one or two partials
 // for the finalize to read back. Measured at 4096 x 768 on MI355X against 4 waves and two
 // workgroups per CU (512 partials): 12.2 against 12.9 us per fused backward (fp32), 9.8
-// against 10.7 us (bf16); 16 waves per workgroup with one row per wave, and a tree
-// reduction over the waves instead of the flat one, were both slower.
+// against 10.7 us (bf16); a tree reduction over the waves instead of the flat one was slower.
 constexpr int gb_waves(int cols) { return cols <= 1024 ? 8 : 4; }
+
+// One row per wave: when every row fits one round of 16-wave workgroups, one per CU
+// (rows <= CUs x 16, cols <= kOneRowMaxCols<T>, so the flat reduction's 16 x 2 x cols floats fit
+// 128 KiB), the gamma/beta backward runs the ONE_ROW form of ln_bwd_reg: no prefetch registers
+// (108 VGPRs at 768 fp32 columns, 4 waves per SIMD), each wave's row in flight at once, still
+// one partial per CU. fp32 rows of 4 vectors per lane (769-1024 columns) would spill at the
+// 128-VGPR limit of 4 waves per SIMD and keep the prefetching form.
+// 4096 x 768 fp32 fused backward on MI355X, one buffer set: 11.87 -> 11.27 us per call (the
+// kernel alone 8.90 -> 8.37 us); eight such waves with two workgroups per CU made the kernel
+// 8.02 us but its 512 partials cost the finalize more than that.
+constexpr int kOneRowWaves = 16;
+template <typename T>
+constexpr int kOneRowMaxCols = T::kPerVec == 4 ? 768 : 1024;
 
 // ------------------------------------------------------------------------------------------
 // Backward, register-resident rows. WRITE_DX: produce grad_x. DO_GB: accumulate the
 // per-workgroup gamma/beta partials into part[blockIdx.x][2 * cols] (gamma then beta).
 // Each wave walks its rows with the next row's dy / x already in flight (software prefetch),
-// so the two wave reductions of one row overlap the loads of the next. dy, x and gamma stay
-// in registers in their storage format and are widened to fp32 where they are used.
+// so the two wave reductions of one row overlap the loads of the next; ONE_ROW drops the
+// prefetch (each row is loaded at the top of its iteration) for grids where each wave has one
+// row. dy, x and gamma stay in registers in their storage format and are widened to fp32
+// where they are used.
 // ------------------------------------------------------------------------------------------
-template <typename T, int VPL, bool WRITE_DX, bool DO_GB, int WAVES>
-__global__ __launch_bounds__(WAVES * HK_WAVE) void ln_bwd_reg(
+template <typename T, int VPL, bool WRITE_DX, bool DO_GB, int WAVES, bool ONE_ROW = false>
+__global__ __launch_bounds__(WAVES * HK_WAVE, ONE_ROW ? 4 : 1) void ln_bwd_reg(
     const uint4* __restrict__ dy, const uint4* __restrict__ x, const float* __restrict__ mean,
     const float* __restrict__ rstd, const uint4* __restrict__ gamma, uint4* __restrict__ dx,
     float* __restrict__ part, int rows, int nvec, float inv_cols) {
@@ -179,8 +194,9 @@ __global__ __launch_bounds__(WAVES * HK_WAVE) void ln_bwd_reg(
       a[k] = d[k] * g[k];
     }
   };
-  if (row < rows) fetch(row);
+  if (!ONE_ROW && row < rows) fetch(row);
   for (; row < rows; row += stride) {
+    if (ONE_ROW) fetch(row);
     uint4 dcur[VPL], xcur[VPL];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
@@ -188,7 +204,7 @@ __global__ __launch_bounds__(WAVES * HK_WAVE) void ln_bwd_reg(
       xcur[i] = xn[i];
     }
     const float m = mn, rs = rn;
-    if (row + stride < rows) fetch(row + stride);
+    if (!ONE_ROW && row + stride < rows) fetch(row + stride);
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
@@ -432,6 +448,21 @@ constexpr int kMaxGbCols = 2048;
 template <typename T>
 constexpr int kMaxBwdVpl = 4096 / (HK_WAVE * T::kPerVec);
 
+// Lets a ONE_ROW gamma/beta backward form use its up to 128 KiB of dynamic LDS (set once per
+// kernel, before its first launch).
+template <typename T, int V, bool WRITE_DX>
+hipError_t one_row_lds_limit() {
+  static std::once_flag once;
+  static hipError_t status = hipSuccess;
+  std::call_once(once, [] {
+    status = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&ln_bwd_reg<T, V, WRITE_DX, true, kOneRowWaves, true>),
+        hipFuncAttributeMaxDynamicSharedMemorySize,
+        static_cast<int>(kOneRowWaves * 2 * kOneRowMaxCols<T> * sizeof(float)));
+  });
+  return status;
+}
+
 // Workgroups of a gamma/beta backward: one per `waves` rows, at most 8 / waves per CU.
 int bwd_gb_grid(int rows, int waves) {
   const int64_t want = hk::ceil_div(rows, waves);
@@ -473,15 +504,19 @@ hipError_t launch_bwd(const St<T>* dy, const St<T>* x, const float* mean, const 
   HK_CHECK_ARG(dy && x && mean && rstd);
   HK_CHECK_ARG(!write_dx || dx);
   // The gamma/beta partials of one workgroup live in LDS: 8 (cols <= 1024) or 4 waves x 2 x
-  // cols floats, kept within 64 KiB (cols <= kMaxGbCols). The backward keeps dy, x and their prefetch in
+  // cols floats, kept within 64 KiB (cols <= kMaxGbCols); the one-row form's 16 waves take up
+  // to 128 KiB (cols <= kOneRowMaxCols<T>). The backward keeps dy, x and their prefetch in
   // registers; past kMaxBwdVpl vectors per lane (4096 columns for every storage type) it would
   // spill, so wider rows take the workgroup-per-row kernels.
   if (reg_path_ok<T>(cols, {dy, x, gamma, dx}) && pick_vpl(cols / T::kPerVec) <= kMaxBwdVpl<T> &&
       (!do_gb || cols <= kMaxGbCols)) {
     const int nvec = cols / T::kPerVec;
-    const int waves = do_gb ? gb_waves(cols) : kWavesPerBlock;
-    const int grid = do_gb ? bwd_gb_grid(rows, waves)
-                           : static_cast<int>(hk::ceil_div(rows, kWavesPerBlock));
+    const bool one_row = do_gb && cols <= kOneRowMaxCols<T> &&
+                         rows <= static_cast<int64_t>(hk::device_cu_count()) * kOneRowWaves;
+    const int waves = one_row ? kOneRowWaves : do_gb ? gb_waves(cols) : kWavesPerBlock;
+    const int grid = one_row ? static_cast<int>(hk::ceil_div(rows, kOneRowWaves))
+                     : do_gb ? bwd_gb_grid(rows, waves)
+                             : static_cast<int>(hk::ceil_div(rows, kWavesPerBlock));
     float* part = nullptr;
     if (do_gb) {
       void* ws = nullptr;
@@ -506,7 +541,17 @@ hipError_t launch_bwd(const St<T>* dy, const St<T>* x, const float* mean, const 
         // kCols <= 1024: the wave count of the gamma/beta forms is fixed by V
         constexpr int kW = gb_waves(kCols);
         if constexpr (kGb) {
-          if (do_gb) {
+          if (do_gb && one_row) {
+            if constexpr (kCols <= kOneRowMaxCols<T>) {
+              const hipError_t attr = write_dx ? one_row_lds_limit<T, V, true>()
+                                               : one_row_lds_limit<T, V, false>();
+              HK_RETURN_IF_ERROR(attr);
+              k = write_dx ? ln_bwd_reg<T, V, true, true, kOneRowWaves, true>
+                           : ln_bwd_reg<T, V, false, true, kOneRowWaves, true>;
+            } else {
+              return hipErrorInvalidValue;  // the smallest VPL holding cols has kCols <= the cap
+            }
+          } else if (do_gb) {
             if (waves != kW) return hipErrorInvalidValue;
             k = write_dx ? ln_bwd_reg<T, V, true, true, kW> : ln_bwd_reg<T, V, false, true, kW>;
           }
