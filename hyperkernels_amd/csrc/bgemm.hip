@@ -612,6 +612,215 @@ __global__ __launch_bounds__(kThreads, 1) void bgemm_mixed(
                                                wg - nfull);
 }
 
+// ---- 256 x 160 tiles on 16 x 16 x 32 MFMAs (A and B both k-major, C = alpha A B^T + ...) ----
+// For products whose 256 x 256 tiles leave CUs idle while 256 x 160 tiles fill one round
+// (8192 x 1280: 160 tiles of 256 x 256, 215 of 192 x 256, 256 of 256 x 160 on 256 CUs). 160
+// columns are 5 blocks of 16, so the waves sit 4 (rows) x 2 (columns), each owning 64 x 80 of C
+// as 4 x 5 blocks of v_mfma_f32_16x16x32_bf16. Whole tiles only (M % 256, N % 160, K % 64 == 0).
+// LDS: a 3-slot ring of k-tiles (3 x 52 KiB, which only this tile shape fits in 160 KiB), each
+// A [256][64 k] then B [160][64 k], bf16, stored as the k-major TileOperand layout (128-byte
+// rows, chunk c of row r at c ^ ((r >> 1) & 7)); a 16-row operand block is one ds_read_b128
+// per lane (lane l: row l % 16, logical chunk 4 s + l / 16 of k step s), 16 consecutive rows
+// per read cycle, conflict-free as in the 32-row form.
+// Copies: A is 32 copy instructions per k-tile (4 per wave), B 20: wave w issues B copies w,
+// w + 8 and, for w < 4, w + 16, so waves 0-3 issue 7 per k-tile and waves 4-7 issue 6 (their
+// vmcnt waits count 6).
+// Per k-tile kt (2 k steps of 32): step 0 reads step 1's operands and runs step 0's 20 MFMAs
+// with the last copies of tile kt + 2 between them; step 1 waits for this wave's copies of
+// tile kt + 1 (tile kt + 2's may still be in flight), meets the others at the barrier (tile
+// kt + 1 visible, slot kt % 3 free), reads tile kt + 1's step-0 operands and issues the first
+// two copies of tile kt + 3 into slot kt % 3 between its MFMAs. Each copy so has more than a
+// k-tile to land and the address unit's work is spread over both steps. On MI355X, 8192 x 1280
+// x 5120: 96.2 us on 215 tiles of 192 x 256, 96.7 with these tiles on a 2-slot ring and every
+// copy in step 1, 90.1 with 3 slots, 92.8 with 3 slots and every copy in step 1, 87.5 as here.
+// The MFMA takes the B block as its first operand, so lane l holds C row l % 16 of its block,
+// columns 4 (l / 16) .. + 3.
+namespace w160 {
+constexpr int kBM = 256, kBN = 160;
+constexpr int kStageA = kBM * BK * 2;  // 32 KiB
+constexpr int kStageB = kBN * BK * 2;  // 20 KiB
+constexpr int kStage = kStageA + kStageB;
+constexpr int kRing = 3;
+constexpr size_t kLdsBytes = kRing * static_cast<size_t>(kStage);  // 156 KiB
+constexpr int kCopiesA = kStageA / 1024 / kWaves;                  // 4
+constexpr int kCopiesB = 3;                                        // 20 over 8 waves, see above
+constexpr int kCopies = kCopiesA + kCopiesB;                       // 7 (6 for waves 4-7)
+constexpr int kFirst = 2;  // copies of a k-tile issued in step 1, the rest in the next step 0
+constexpr int kBlkM = 4, kBlkN = 5;                             // 16 x 16 blocks per wave
+constexpr int kWaveM = 16 * kBlkM, kWaveN = 16 * kBlkN;         // 64 x 80
+constexpr int kPitch = kWaveN * 4 + 16;                         // fp32 staging row, bytes
+static_assert(kStageB / 1024 == 20 && kCopiesA * kWaves * 1024 == kStageA, "copy split");
+static_assert(kLdsBytes <= 160 * 1024, "fits gfx950's 160 KiB of LDS");
+static_assert(kWaves * 16 * kPitch <= static_cast<int>(kLdsBytes), "staging fits");
+
+// LDS byte offset of lane `lane`'s 16 bytes of the 16-row block at row `r0`, k step s (0, 1).
+__device__ __forceinline__ int frag16(int r0, int s, int lane) {
+  const int row = r0 + (lane & 15);
+  const int c = 4 * s + (lane >> 4);
+  return row * 128 + ((c ^ ((row >> 1) & 7)) << 4);
+}
+}  // namespace w160
+
+__global__ __launch_bounds__(kThreads, 1) void bgemm_nt_w160(
+    int M, int N, int K, Epi ep, const uint16_t* __restrict__ A, int64_t lda, int64_t sA,
+    const uint16_t* __restrict__ B, int64_t ldb, int64_t sB, uint16_t* __restrict__ C,
+    int64_t ldc, int64_t sC) {
+  using namespace w160;
+  using OK = TileOperand<true>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
+  unsigned char HK_LDS* lds = (unsigned char HK_LDS*)lds_raw;
+  const int batch = blockIdx.z;
+  const int tiles_m = M / kBM, tiles_n = N / kBN;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const unsigned char* gA = reinterpret_cast<const unsigned char*>(
+      A + static_cast<int64_t>(batch) * sA + static_cast<int64_t>(m0) * lda);
+  const unsigned char* gB = reinterpret_cast<const unsigned char*>(
+      B + static_cast<int64_t>(batch) * sB + static_cast<int64_t>(n0) * ldb);
+  // per-lane source offsets (bytes, from the tile base at k = 0) and LDS destinations of this
+  // wave's copies; rows stay inside the tile (whole tiles), so no clamping is needed
+  int off[kCopies];
+  unsigned dst[kCopies];
+  const unsigned lds_addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
+#pragma unroll
+  for (int q = 0; q < kCopies; ++q) {
+    int row, k;
+    if (q < kCopiesA) {
+      const int ii = wave * kCopiesA + q;
+      OK::source(ii, lane, row, k);
+      off[q] = static_cast<int>(OK::byte_offset(row, k, lda));
+      dst[q] = lds_addr + ii * 1024;
+    } else {
+      int ii = wave + 8 * (q - kCopiesA);
+      if (ii >= 20) ii = wave + 8;  // waves 4-7 have no third B copy (never issued)
+      OK::source(ii, lane, row, k);
+      off[q] = static_cast<int>(OK::byte_offset(row, k, ldb));
+      dst[q] = lds_addr + kStageA + ii * 1024;
+    }
+  }
+  const int ktiles = K / BK;
+  const bool six = wave >= 4;  // waves 4-7 issue 6 copies per k-tile
+  auto copy = [&](int kt, int slot, int q) {
+    if (q == kCopies - 1 && six) return;
+    const unsigned char* base = (q < kCopiesA ? gA : gB) + kt * (2 * BK);
+    copy16_to_lds(base, off[q], dst[q] + slot * kStage);
+  };
+  // wait until at most n k-tiles of this wave's copies are in flight
+  auto wait_tiles = [&](int n) {
+    if (n == 2) {
+      if (six) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * kCopies - 2) : "memory");
+      else asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * kCopies) : "memory");
+    } else if (n == 1) {
+      if (six) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kCopies - 1) : "memory");
+      else asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kCopies) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    }
+  };
+
+  f32x4_t acc[kBlkM][kBlkN];
+#pragma unroll
+  for (int i = 0; i < kBlkM; ++i)
+#pragma unroll
+    for (int j = 0; j < kBlkN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int p = 0; p < kRing; ++p)
+    if (p < ktiles) {
+#pragma unroll
+      for (int q = 0; q < kCopies; ++q) copy(p, p, q);
+    }
+  wait_tiles(ktiles >= 3 ? 2 : ktiles - 1);  // k-tile 0 landed
+  __builtin_amdgcn_s_barrier();
+
+  bf16x8_t fa[2][kBlkM], fb[2][kBlkN];
+  auto read_ops = [&](int slot, int s, int buf) {
+    const unsigned char HK_LDS* sa = lds + slot * kStage;
+    const unsigned char HK_LDS* sb = sa + kStageA;
+#pragma unroll
+    for (int i = 0; i < kBlkM; ++i)
+      fa[buf][i] = *reinterpret_cast<const bf16x8_t HK_LDS*>(
+          sa + frag16(wm * kWaveM + 16 * i, s, lane));
+#pragma unroll
+    for (int j = 0; j < kBlkN; ++j)
+      fb[buf][j] = *reinterpret_cast<const bf16x8_t HK_LDS*>(
+          sb + frag16(wn * kWaveN + 16 * j, s, lane));
+  };
+  read_ops(0, 0, 0);
+  int slot = 0;
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int nslot = slot == kRing - 1 ? 0 : slot + 1;
+    const int slot2 = nslot == kRing - 1 ? 0 : nslot + 1;
+    // step 0: operands of step 1 read while step 0 multiplies, with the rest of tile kt + 2's
+    // copies between the MFMAs (its first kFirst went out in tile kt - 1's step 1; tile 2's
+    // all in the prologue)
+    const bool rest = kt >= 1 && kt + 2 < ktiles;
+    read_ops(slot, 1, 1);
+#pragma unroll
+    for (int i = 0; i < kBlkM; ++i)
+#pragma unroll
+      for (int j = 0; j < kBlkN; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[0][j], fa[0][i], acc[i][j], 0, 0,
+                                                            0);
+        const int q = kFirst + 2 * (i * kBlkN + j);
+        if (q < kCopies && rest) copy(kt + 2, slot2, q);
+        if (q + 1 < kCopies && rest) copy(kt + 2, slot2, q + 1);
+      }
+    // step 1: tile kt + 1 landed (tile kt + 2's copies may still be in flight), slot free
+    wait_tiles(kt + 2 < ktiles ? 1 : 0);
+    __builtin_amdgcn_s_barrier();
+    if (kt + 1 < ktiles) read_ops(nslot, 0, 0);
+    const bool more = kt + kRing < ktiles;
+#pragma unroll
+    for (int i = 0; i < kBlkM; ++i)
+#pragma unroll
+      for (int j = 0; j < kBlkN; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[1][j], fa[1][i], acc[i][j], 0, 0,
+                                                            0);
+        const int q = i * kBlkN + j;
+        if (q < kFirst && more) copy(kt + kRing, slot, q);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    slot = nslot;
+  }
+
+  // Epilogue: each wave stages one 16-row block row (16 x 80 fp32) in its own LDS area and
+  // reads it back as 8 consecutive columns per lane (10 lanes per row, 6 rows per pass), so the
+  // bf16 outputs go out 16 bytes per lane in row segments.
+  __syncthreads();
+  unsigned char HK_LDS* area = lds + wave * (16 * kPitch);
+  uint16_t* Cb = C + static_cast<int64_t>(batch) * sC;
+  const int wrow0 = m0 + wm * kWaveM, wcol0 = n0 + wn * kWaveN;
+  auto emit = [&](auto&& out) {
+#pragma unroll
+    for (int i = 0; i < kBlkM; ++i) {
+#pragma unroll
+      for (int j = 0; j < kBlkN; ++j)
+        *reinterpret_cast<f32x4_t HK_LDS*>(area + (lane & 15) * kPitch +
+                                          (16 * j + 4 * (lane >> 4)) * 4) = acc[i][j];
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        const int rr = 6 * p + lane / 10, cc = (lane % 10) * 8;
+        if (lane < 60 && rr < 16) {
+          const f32x4_t a = *reinterpret_cast<const f32x4_t HK_LDS*>(area + rr * kPitch + cc * 4);
+          const f32x4_t b =
+              *reinterpret_cast<const f32x4_t HK_LDS*>(area + rr * kPitch + cc * 4 + 16);
+          out(16 * i + rr, cc, a, b);
+        }
+      }
+    }
+  };
+  if (ep.bias)
+    emit(Bf16RowOut<true>{ep, Cb, ldc, M, N, wrow0, wcol0});
+  else
+    emit(Bf16RowOut<false>{ep, Cb, ldc, M, N, wrow0, wcol0});
+}
+
 // C = alpha * sum_s part[s] + beta * C (split order), fp32 -> bf16.
 // I: the index type, uint32_t when every index of the launch fits in 31 bits (a 64-bit
 // division costs several times a 32-bit one).
@@ -787,6 +996,35 @@ int row_tile(bool ta, int M, int N, int grid_z, int split_k) {
   return 0.75 * static_cast<double>(hk::ceil_div(t192, cus)) <= 0.9 ? 192 : 256;
 }
 
+// 256 x 160 tiles (bgemm_nt_w160): both operands k-major, one k split, bf16 C, whole tiles,
+// when 256 x 256 tiles leave CUs idle and 256 x 160 tiles fit one round. Each such workgroup
+// carries 5/8 of a 256 x 256 tile's work (3/4 for the 192-row tiles, which then give way).
+bool w160_plan(bool ta, bool tb, int M, int N, int K, int grid_z, int split_k) {
+  if (ta || !tb || split_k != 1) return false;
+  if (M % w160::kBM != 0 || N % w160::kBN != 0 || K % BK != 0) return false;
+  const int64_t cus = hk::device_cu_count();
+  const int64_t t256 = static_cast<int64_t>((M + 255) / 256) * ((N + BN - 1) / BN) * grid_z;
+  const int64_t t160 = static_cast<int64_t>(M / w160::kBM) * (N / w160::kBN) * grid_z;
+  return t256 < cus && t160 <= cus;
+}
+
+hipError_t launch_w160(int grid_z, hipStream_t stream, int M, int N, int K, const Epi& ep,
+                       const uint16_t* A, int64_t lda, int64_t sA, const uint16_t* B,
+                       int64_t ldb, int64_t sB, uint16_t* C, int64_t ldc, int64_t sC) {
+  static std::once_flag once;
+  static hipError_t attr_status = hipSuccess;
+  std::call_once(once, [] {
+    attr_status = hipFuncSetAttribute(reinterpret_cast<const void*>(&bgemm_nt_w160),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(w160::kLdsBytes));
+  });
+  HK_RETURN_IF_ERROR(attr_status);
+  const dim3 grid(static_cast<unsigned>((M / w160::kBM) * (N / w160::kBN)), 1, grid_z);
+  hipLaunchKernelGGL(bgemm_nt_w160, grid, dim3(kThreads), w160::kLdsBytes, stream, M, N, K, ep,
+                     A, lda, sA, B, ldb, sB, C, ldc, sC);
+  return hk::launch_status();
+}
+
 // The product over its column regions (column_split), in one launch; grid.z covers batches
 // and splits. A split into partials (P with split_k > 1) keeps one region.
 template <bool P>
@@ -794,6 +1032,10 @@ hipError_t run_regions(bool ta, bool tb, int grid_z, hipStream_t stream, int M, 
                        const Epi& ep, const uint16_t* A, int64_t lda, int64_t sA,
                        const uint16_t* B, int64_t ldb, int64_t sB, uint16_t* C, int64_t ldc,
                        int64_t sC, int split_k, int kps, float* part, const hk::F32Out& fo) {
+  if constexpr (!P) {
+    if (w160_plan(ta, tb, M, N, K, grid_z, split_k))
+      return launch_w160(grid_z, stream, M, N, K, ep, A, lda, sA, B, ldb, sB, C, ldc, sC);
+  }
   if (row_tile(ta, M, N, grid_z, split_k) == 192) {
     const int64_t tiles = static_cast<int64_t>((M + 191) / 192) * ((N + BN - 1) / BN);
     const dim3 grid(static_cast<unsigned>(tiles), 1, grid_z);
@@ -1007,7 +1249,17 @@ extern "C" int hk_bgemm_tile_rows(int transA, int transB, int M, int N, int K, i
       !tiled_path(ta, tb, M, N, K, lda, ldb, N, lda * (ta ? K : M), ldb * (tb ? N : K),
                   static_cast<int64_t>(M) * N, true))
     return 0;
+  if (w160_plan(ta, tb, M, N, K, batchCount * splits, splits)) return w160::kBM;
   return row_tile(ta, M, N, batchCount * splits, splits);
+}
+
+extern "C" int hk_bgemm_tile_cols(int transA, int transB, int M, int N, int K, int batchCount,
+                                  int splitK) {
+  const int rows = hk_bgemm_tile_rows(transA, transB, M, N, K, batchCount, splitK);
+  if (rows <= 0) return rows;
+  const int splits = hk_bgemm_split_count(transA, transB, M, N, K, batchCount, splitK);
+  return w160_plan(transA != 0, transB != 0, M, N, K, batchCount * splits, splits) ? w160::kBN
+                                                                                   : BN;
 }
 
 extern "C" hipError_t hk_bgemm(int transA, int transB, int M, int N, int K, hk_bf16 alpha,

@@ -323,8 +323,14 @@ HK_API int hk_bgemm_split_count(int transA, int transB, int M, int N, int K, int
  * hk_bgemm_split_count) returns the rows per output tile the MFMA path runs a product of this
  * shape with: 256, or 192 when 256-row tiles would leave most CUs idle and A is k-major
  * (transA == 0); 0 for the GEMV and fallback kernels or an empty product, -1 for an invalid
- * argument. */
+ * argument. hk_bgemm_tile_cols (likewise a host-only query) returns the columns per output
+ * tile: 160 when both operands are k-major (transA == 0, transB != 0), the product runs in one
+ * k split, M, N and K are multiples of 256, 160 and 64, and 256 x 256 tiles would leave CUs
+ * idle while 256 x 160 tiles fit one round (the 8192 x 1280 x 5120 dA product); otherwise 256
+ * (the last tile columns may run 128 wide); 0 / -1 as hk_bgemm_tile_rows. */
 HK_API int hk_bgemm_tile_rows(int transA, int transB, int M, int N, int K, int batchCount,
+                              int splitK);
+HK_API int hk_bgemm_tile_cols(int transA, int transB, int M, int N, int K, int batchCount,
                               int splitK);
 
 /* ------------------------------------------------------------------------------------------

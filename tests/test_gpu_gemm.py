@@ -130,10 +130,11 @@ def test_bgemm_backward_baseline_shapes_library_split(hk, orc, which):
         fn, (M, N, K), (ta, tb) = "hk_bgemm_tn_backward", (1280, 5120, 8192), (1, 0)
     splits = lib.hk_bgemm_split_count(ta, tb, M, N, K, 1, 0)
     rows = lib.hk_bgemm_tile_rows(ta, tb, M, N, K, 1, 0)
-    say("bgemm backward baseline", which, "splits", splits, "tile rows", rows)
+    cols = lib.hk_bgemm_tile_cols(ta, tb, M, N, K, 1, 0)
+    say("bgemm backward baseline", which, "splits", splits, "tile", rows, "x", cols)
     assert splits == (1 if which == "dA_NT" else 2)
-    # dA's 160 tiles of 256 rows leave 96 CUs idle: it runs on 215 tiles of 192 rows
-    assert rows == (192 if which == "dA_NT" else 256)
+    # dA's 160 tiles of 256 x 256 leave 96 CUs idle: it runs on 256 tiles of 256 x 160
+    assert (rows, cols) == ((256, 160) if which == "dA_NT" else (256, 256))
     A, B, C0 = _operands(orc, M, N, K, ta, tb, 1000 + M, normal=True)
     first = _run(hk, fn, A, B, C0, M, N, K, ta, tb, 1.0, 0.5)
     second = _run(hk, fn, A, B, C0, M, N, K, ta, tb, 1.0, 0.5)
@@ -162,12 +163,67 @@ def test_bgemm_192_row_tiles(hk, orc, M, N, K, ta, tb):
 
 def test_bgemm_tile_rows_query(hk):
     lib = hk.lib()
+    # 256 x 160 tiles: NT, one split, whole tiles, 256 x 256 tiles under one round, 256 x 160
+    # tiles within one
+    assert (lib.hk_bgemm_tile_rows(0, 1, 8192, 1280, 5120, 1, 0),
+            lib.hk_bgemm_tile_cols(0, 1, 8192, 1280, 5120, 1, 0)) == (256, 160)
+    assert lib.hk_bgemm_tile_cols(0, 0, 8192, 1280, 5120, 1, 0) == 256  # B not k-major
+    assert lib.hk_bgemm_tile_cols(0, 1, 8192, 1280, 5112, 1, 0) == 256  # K % 64 != 0
+    assert lib.hk_bgemm_tile_cols(0, 1, 8192, 1440, 5120, 1, 0) == 256  # 288 tiles of 160
+    assert lib.hk_bgemm_tile_cols(0, 1, 8192, 5120, 1280, 1, 0) == 256  # 256-wide fill
+    assert lib.hk_bgemm_tile_cols(0, 1, 8192, 1280, 5120, 1, 2) == 256  # explicit split
+    assert lib.hk_bgemm_tile_cols(0, 1, 1, 512, 512, 1, 0) == 0  # GEMV
+    assert lib.hk_bgemm_tile_cols(0, 1, -1, 512, 512, 1, 0) == -1
     assert lib.hk_bgemm_tile_rows(0, 0, 8192, 5120, 1280, 1, 0) == 256  # 640 tiles: 2.5 rounds
     assert lib.hk_bgemm_tile_rows(1, 0, 512, 512, 512, 1, 0) == 256  # M-major A
     assert lib.hk_bgemm_tile_rows(0, 0, 512, 512, 512, 1, 4) == 256  # split K
     assert lib.hk_bgemm_tile_rows(0, 0, 1, 512, 512, 1, 0) == 0  # GEMV
     assert lib.hk_bgemm_tile_rows(0, 0, 0, 512, 512, 1, 0) == 0
     assert lib.hk_bgemm_tile_rows(0, 0, -1, 512, 512, 1, 0) == -1
+
+
+@pytest.mark.parametrize("M,N,K,batch", [(256, 160, 64, 1), (512, 320, 128, 1),
+                                         (1024, 800, 320, 1), (2048, 1280, 192, 1),
+                                         (512, 480, 256, 2)])
+def test_bgemm_256x160_tiles(hk, orc, M, N, K, batch):
+    # NT products (both operands k-major) that run on 256 x 160 tiles of 16 x 16 x 32 MFMAs:
+    # one tile up to 64, batched, alpha and beta active; each batch against its own product
+    lib = hk.lib()
+    assert lib.hk_bgemm_tile_rows(0, 1, M, N, K, batch, 0) == 256
+    assert lib.hk_bgemm_tile_cols(0, 1, M, N, K, batch, 0) == 160
+    say("bgemm 256x160 tiles", M, N, K, batch)
+    ops = [_operands(orc, M, N, K, 0, 1, 1300 + 10 * b) for b in range(batch)]
+    dA = to_dev_bf16(np.stack([o[0] for o in ops]))
+    dB = to_dev_bf16(np.stack([o[1] for o in ops]))
+    dC = to_dev_bf16(np.stack([o[2] for o in ops]))
+    st = lib.hk_bgemm(0, 1, M, N, K, bits(1.5), dA.data_ptr(), K, M * K, dB.data_ptr(), K, N * K,
+                      bits(0.5), dC.data_ptr(), N, M * N, batch,
+                      torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    out = to_host_bits(dC)
+    for b, (A, B, C0) in enumerate(ops):
+        _check(orc, out[b], A, B, C0, 0, 1, 1.5, 0.5)
+
+
+@pytest.mark.parametrize("bias_numel", ["M", "N"])
+def test_bgemm_256x160_tiles_bias_and_backward_entry(hk, orc, bias_numel):
+    # the bias form (C written, not read) and the dA entry point on 256 x 160 tiles
+    M, N, K = 1024, 640, 256
+    lib = hk.lib()
+    assert lib.hk_bgemm_tile_cols(0, 1, M, N, K, 1, 1) == 160
+    say("bgemm 256x160 bias", bias_numel)
+    A, B, C0 = _operands(orc, M, N, K, 0, 1, 1400)
+    n = M if bias_numel == "M" else N
+    bias = orc.f32_to_bf16(orc.splitmix_uniform(n, 1401))
+    dA, dB, dC, dbias = to_dev_bf16(A), to_dev_bf16(B), to_dev_bf16(C0), to_dev_bf16(bias)
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.hk_bgemm_core_bias(0, 1, M, N, K, bits(1.0), dA.data_ptr(), K, 0, dB.data_ptr(),
+                                  K, 0, bits(2.0), dbias.data_ptr(), n, dC.data_ptr(), N, 0, 1,
+                                  stream) == 0
+    ref = orc.bgemm(0, 1, A, B, alpha=1.0, beta=2.0, bias=bias)
+    assert max_rel(orc.bf16_to_f32(to_host_bits(dC)), ref) <= 1e-2
+    _check(orc, _run(hk, "hk_bgemm_nt_backward", A, B, C0, M, N, K, 0, 1, 1.0, 0.5), A, B, C0,
+           0, 1, 1.0, 0.5)
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
