@@ -1,7 +1,8 @@
-"""Seeded random-shape GPU parity sweep: BF16 BGEMM (every layout, batches, alpha / beta),
-FP32 SGEMM (every layout, split-K, bias forms) and attention forward + backward (ragged T,
-causal and not, strided [B, T, nh, d] views), each against the oracle at the same tolerances
-as the fixed-shape tests (1e-2 for bf16 outputs, 2e-3 for fp32 ones, max|err| / max|ref|).
+"""Seeded random-shape GPU parity sweep: BF16 BGEMM (every layout, batches, alpha / beta, and NT
+products on whole 256 x 160 tiles), FP32 SGEMM (every layout, split-K, bias forms) and attention
+forward + backward (ragged T, causal and not, strided [B, T, nh, d] views), each against the
+oracle at the same tolerances as the fixed-shape tests (1e-2 for bf16 outputs, 2e-3 for fp32
+ones, max|err| / max|ref|).
 
 The shapes are drawn once, from a fixed seed, when the module is collected, so every run sees
 the same cases and a failing case is named by its parameters. The draws mix 8-aligned extents
@@ -54,6 +55,39 @@ def test_bgemm_random_shapes(hk, orc, M, N, K, ta, tb, batch, alpha, beta, seed)
     out = to_host_bits(dC)
     for b, (A, B, C0) in enumerate(ops):
         _check(orc, out[b], A, B, C0, ta, tb, alpha, beta)
+
+
+def _w160_cases(n=10, seed=20261205):
+    # NT products of whole 256 x 160 tiles that fit one round (the 16 x 16 x 32 MFMA kernel)
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        M, N = 256 * int(rng.integers(1, 9)), 160 * int(rng.integers(1, 9))
+        K, batch = 64 * int(rng.integers(1, 12)), int(rng.integers(1, 4))
+        if (M // 256) * (N // 160) * batch > 256 or -(-M // 256) * -(-N // 256) * batch >= 256:
+            continue
+        alpha = float(rng.choice([1.0, 0.5, -1.25, 2.0]))
+        beta = float(rng.choice([0.0, 0.5, 1.0, -0.75]))
+        cases.append((M, N, K, batch, alpha, beta, 3500 + 10 * len(cases)))
+    return cases
+
+
+@pytest.mark.parametrize("M,N,K,batch,alpha,beta,seed", _w160_cases())
+def test_bgemm_random_256x160_tiles(hk, orc, M, N, K, batch, alpha, beta, seed):
+    lib = hk.lib()
+    assert lib.hk_bgemm_tile_cols(0, 1, M, N, K, batch, 0) == 160
+    say("bgemm random 256x160", M, N, K, batch, alpha, beta)
+    ops = [_operands(orc, M, N, K, 0, 1, seed + b) for b in range(batch)]
+    dA = to_dev_bf16(np.stack([o[0] for o in ops]))
+    dB = to_dev_bf16(np.stack([o[1] for o in ops]))
+    dC = to_dev_bf16(np.stack([o[2] for o in ops]))
+    st = lib.hk_bgemm(0, 1, M, N, K, bits(alpha), dA.data_ptr(), K, M * K, dB.data_ptr(), K,
+                      N * K, bits(beta), dC.data_ptr(), N, M * N, batch,
+                      torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    out = to_host_bits(dC)
+    for b, (A, B, C0) in enumerate(ops):
+        _check(orc, out[b], A, B, C0, 0, 1, alpha, beta)
 
 
 def _sgemm_cases(n=18, seed=20261203):
